@@ -1,0 +1,179 @@
+/* qwen_gpu_ext — DiT-path dispatch entry points (reference qwen_gpu_ext.h)
+ * over the HIP runtime of h3_gpu.h, plus the fused MI355X entry points the
+ * DiT host uses (declared after the reference-named ones).
+ *
+ * All activations are bf16 row-major [rows, features] with heads interleaved
+ * as [row, head, 128]; RoPE tables are fp32 [rows, 64]; row_map is u32. */
+#ifndef QWEN_GPU_EXT_H
+#define QWEN_GPU_EXT_H
+
+#include "h3_gpu.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* reference qwen_gpu_ext.h:11-16 (kernel h3_shaders.metal:4767-4815) */
+int qw_gpu_layer_norm_mod_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                               const h3_gpu_tensor *input,
+                               const h3_gpu_tensor *modulation,
+                               const h3_gpu_tensor *row_map, uint32_t rows,
+                               uint32_t width, uint32_t slots,
+                               uint32_t scale_slot, float epsilon);
+/* reference qwen_gpu_ext.h:19-22 (h3_shaders.metal:4817-4850) */
+int qw_gpu_rms_norm_one_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                             const h3_gpu_tensor *input,
+                             const h3_gpu_tensor *weight, uint32_t rows,
+                             uint32_t width, float epsilon);
+/* reference qwen_gpu_ext.h:25-26 */
+int qw_gpu_tanh_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                     const h3_gpu_tensor *input, uint32_t elements);
+/* reference qwen_gpu_ext.h:30-36 (h3_shaders.metal:4864-4896). In place
+ * only (query_output == query_input, key_output == key_input). */
+int qw_gpu_qk_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *query_output,
+                        h3_gpu_tensor *key_output,
+                        const h3_gpu_tensor *query_input,
+                        const h3_gpu_tensor *key_input,
+                        const h3_gpu_tensor *rope_cos,
+                        const h3_gpu_tensor *rope_sin, uint32_t sequence,
+                        uint32_t heads, uint32_t head_dim);
+/* reference qwen_gpu_ext.h:65-67 (h3_shaders.metal:5078-5095) */
+int qw_gpu_swiglu_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                       const h3_gpu_tensor *fc1, uint32_t rows,
+                       uint32_t width);
+/* reference qwen_gpu_ext.h:118-125: query rows against every key. */
+int qw_gpu_flash_sdpa_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                           const h3_gpu_tensor *query,
+                           const h3_gpu_tensor *key,
+                           const h3_gpu_tensor *value, uint32_t q_rows,
+                           uint32_t kv_rows, uint32_t heads,
+                           uint32_t head_dim, float scale);
+/* reference qwen_gpu_ext.h:131-138: per-row prefix limits (u32). Grouped
+ * K/V heads are not on the DiT path: kv_heads must equal heads. */
+int qw_gpu_flash_sdpa_prefix_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                                  const h3_gpu_tensor *query,
+                                  const h3_gpu_tensor *key,
+                                  const h3_gpu_tensor *value,
+                                  const h3_gpu_tensor *kv_limit,
+                                  uint32_t q_rows, uint32_t kv_rows,
+                                  uint32_t heads, uint32_t kv_heads,
+                                  uint32_t head_dim, float scale);
+/* reference qwen_gpu_ext.h:204-210: q/k/v = X W_{q,k,v}^T, three outputs. */
+int qw_gpu_qkv_bf16(h3_gpu *gpu, h3_gpu_tensor *query_out,
+                    h3_gpu_tensor *key_out, h3_gpu_tensor *value_out,
+                    const h3_gpu_tensor *input,
+                    const h3_gpu_tensor *query_weight,
+                    const h3_gpu_tensor *key_weight,
+                    const h3_gpu_tensor *value_weight, uint32_t rows,
+                    uint32_t dim);
+/* reference qwen_gpu_ext.h:223-228: image rows against the full prefix. */
+int qw_gpu_sdpa_rect_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                          const h3_gpu_tensor *query,
+                          const h3_gpu_tensor *key,
+                          const h3_gpu_tensor *value,
+                          uint32_t query_sequence, uint32_t kv_sequence,
+                          uint32_t heads, uint32_t head_dim, float scale);
+
+/* ---- MI355X fused entry points (no reference counterpart) ------------- */
+
+/* Shift-variant LayerNorm modulation: LN(x) * (1 + scale) + shift.
+ * shift_slot < 0 disables the shift (then identical to the call above). */
+int qw_gpu_layer_norm_mod_shift_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                                     const h3_gpu_tensor *input,
+                                     const h3_gpu_tensor *modulation,
+                                     const h3_gpu_tensor *row_map,
+                                     uint32_t rows, uint32_t width,
+                                     uint32_t slots, uint32_t scale_slot,
+                                     int32_t shift_slot, float epsilon);
+
+enum { QW_LINEAR_STORE = 0, QW_LINEAR_GELU = 1, QW_LINEAR_GATE = 2 };
+
+/* One GEMM with a fused epilogue, on sub-ranges of tensors:
+ *   y = bf16( X W^T * wscale + bias )                  (STORE)
+ *   y = bf16( gelu_tanh( bf16(X W^T * wscale + bias) ) ) (GELU)
+ *   out = bf16( out + bf16(X W^T * wscale + bias) * gate ) (GATE, in place;
+ *         gate row = row_map[r], columns gate_slot*cols..)
+ * weight is bf16 [cols, k] or int8 [cols, k] (then wscale f32 [cols] is
+ * required). Offsets/strides are in elements; k must be a multiple of 64. */
+typedef struct {
+    h3_gpu_tensor *out;
+    size_t out_offset;
+    uint32_t ldc;
+    const h3_gpu_tensor *in;
+    size_t in_offset;
+    uint32_t lda;
+    const h3_gpu_tensor *weight;
+    const h3_gpu_tensor *wscale;
+    const h3_gpu_tensor *bias;
+    uint32_t rows, k, cols;
+    int epilogue;
+    const h3_gpu_tensor *modulation; /* GATE */
+    const h3_gpu_tensor *row_map;    /* GATE */
+    uint32_t slots, gate_slot;       /* GATE: row stride slots*cols */
+} qw_linear_desc;
+int qw_gpu_linear(h3_gpu *gpu, const qw_linear_desc *desc);
+
+/* Fused per-head RMSNorm (single rounding, h3_shaders.metal:4309-4329) and
+ * interleaved RoPE (h3_shaders.metal:4864-4896) over q and k in one
+ * strided buffer [rows, ld]: q heads at column 0, k heads at k_offset.
+ * Table row = row % rope_rows. norm_q/norm_k NULL skips the norm; rope NULL
+ * skips the rotation. In place. */
+int qw_gpu_qk_norm_rope_bf16(h3_gpu *gpu, h3_gpu_tensor *qk, uint32_t rows,
+                             uint32_t heads, uint32_t ld, uint32_t k_offset,
+                             const h3_gpu_tensor *norm_q,
+                             const h3_gpu_tensor *norm_k,
+                             const h3_gpu_tensor *rope_cos,
+                             const h3_gpu_tensor *rope_sin,
+                             uint32_t rope_rows, float epsilon);
+
+/* Batched block-causal flash attention over strided q/k/v views (e.g. the
+ * fused [rows, 3H] projection): batch entries of q_rows queries / kv_rows
+ * keys stacked along rows. kv_limit (u32 [q_rows], shared by the batch)
+ * overrides the t2i closed form (text rows causal or full-prefix, image
+ * rows all keys). */
+typedef struct {
+    h3_gpu_tensor *out;
+    size_t out_offset;
+    uint32_t ldo;
+    const h3_gpu_tensor *q, *k, *v;
+    size_t q_offset, k_offset, v_offset;
+    uint32_t ldq, ldk, ldv;
+    const h3_gpu_tensor *kv_limit;
+    uint32_t batch, q_rows, kv_rows, heads;
+    uint32_t text_rows;
+    int text_causal;
+    float scale;
+} qw_attention_desc;
+int qw_gpu_attention_bf16(h3_gpu *gpu, const qw_attention_desc *desc);
+
+/* qwen_dit.m:1159-1186 on device: raw modulation [mod_rows, S*hidden] ->
+ * slot layout with tanh'd gates stored by truncation. S = 4, or 6 when
+ * shift_variant (then slots 4, 5 carry the shifts). */
+int qw_gpu_modulation_reorder_bf16(h3_gpu *gpu, h3_gpu_tensor *slots_out,
+                                   const h3_gpu_tensor *raw,
+                                   uint32_t mod_rows, uint32_t hidden,
+                                   int shift_variant);
+
+/* Seeded synthetic values: bf16(std * z + offset), z from the counter-based
+ * generator keyed by (seed, stream, index) — bit-identical to the host
+ * restatement used by the tests. Fills [offset_elems, +count). */
+int qw_gpu_fill_normal_bf16(h3_gpu *gpu, h3_gpu_tensor *tensor,
+                            size_t offset_elems, size_t count, uint64_t seed,
+                            uint64_t stream, float std, float offset);
+
+/* Dequantised int8 weight q * scale as fp32 [rows, cols]. */
+int qw_gpu_dequant_int8_f32(h3_gpu *gpu, h3_gpu_tensor *output,
+                            const h3_gpu_tensor *q,
+                            const h3_gpu_tensor *scales, uint32_t rows,
+                            uint32_t cols);
+
+/* Strided row copy: rows x row_elems of dtype-size elements. */
+int qw_gpu_copy_rows(h3_gpu *gpu, h3_gpu_tensor *dst, size_t dst_offset,
+                     uint32_t dst_stride, const h3_gpu_tensor *src,
+                     size_t src_offset, uint32_t src_stride, uint32_t rows,
+                     uint32_t row_elems);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

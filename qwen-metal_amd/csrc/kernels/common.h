@@ -1,0 +1,75 @@
+/* Shared device helpers for the gfx950 kernels (wave64, CDNA4). */
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../qw_kernel_args.h"
+
+typedef uint16_t u16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define QW_KERNEL extern "C" __global__
+
+__device__ __forceinline__ float bf2f(u16 b) {
+    return __uint_as_float((uint32_t)b << 16);
+}
+
+/* Round-to-nearest-even to bf16 by integer bias (finite inputs), the same
+ * rounding as the reference's h3_f32_to_bf16. */
+__device__ __forceinline__ u16 f2bf(float f) {
+    uint32_t b = __float_as_uint(f);
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return (u16)(b >> 16);
+}
+
+__device__ __forceinline__ u16 f2bf_trunc(float f) {
+    return (u16)(__float_as_uint(f) >> 16);
+}
+
+/* Low/high bf16 halves of a packed 32-bit word. */
+__device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+/* Block-wide sum; red must hold blockDim.x / 64 floats. Result in all lanes. */
+__device__ __forceinline__ float block_sum(float v, float *red) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int waves = (blockDim.x + 63) >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < waves; i++) s += red[i];
+    return s;
+}
+
+/* h3_shaders.metal:3385-3408 (approximate = 1): GELU with the tanh form,
+ * saturating outside |inner| < 10. */
+__device__ __forceinline__ float gelu_tanh_f(float v) {
+    float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    if (inner <= -10.0f) return 0.0f;
+    if (inner >= 10.0f) return v;
+    return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }

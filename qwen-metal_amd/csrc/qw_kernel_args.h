@@ -1,0 +1,141 @@
+/* Kernel argument blocks shared by the host runtime (h3_gpu_hip.cpp) and
+ * the gfx950 code object (qwen_kernels.hip). Every kernel takes exactly one
+ * of these by value, so hipModuleLaunchKernel passes a single parameter. */
+#ifndef QW_KERNEL_ARGS_H
+#define QW_KERNEL_ARGS_H
+
+#include <stdint.h>
+
+#define QW_HEAD_DIM 128
+
+/* GEMM epilogues: y = acc * wscale[n] + bias[n] rounded to bf16, then */
+enum {
+    QW_EPI_STORE = 0, /* store y */
+    QW_EPI_GELU = 1,  /* store bf16(gelu_tanh(y)) */
+    QW_EPI_GATE = 2   /* out = bf16(out + y * gate[row_map[r]][n]) in place */
+};
+
+typedef struct {
+    const void *a;        /* bf16 [m, k], row stride lda */
+    const void *w;        /* bf16 or int8 [n, k], row stride k */
+    const float *wscale;  /* int8: per-row scale [n]; NULL for bf16 */
+    const uint16_t *bias; /* bf16 [n] or NULL */
+    uint16_t *out;        /* bf16 [m, n], row stride ldc */
+    const uint16_t *gate; /* QW_EPI_GATE: modulation base (slot offset applied) */
+    const uint32_t *row_map;
+    uint32_t m, n, k;
+    uint32_t lda, ldc;
+    uint32_t gate_row_stride; /* elements between modulation rows */
+    uint32_t tiles_m, tiles_n;
+} qw_gemm_args;
+
+typedef struct {
+    uint16_t *out;
+    const uint16_t *in;
+    const uint16_t *modulation; /* [mod_rows, slots * width] */
+    const uint32_t *row_map;
+    uint32_t rows, width, slots, scale_slot;
+    int32_t shift_slot; /* < 0: none */
+    float eps;
+} qw_ln_mod_args;
+
+typedef struct {
+    uint16_t *out;
+    const uint16_t *in;
+    const uint16_t *weight; /* effective weight = weight + 1 */
+    uint32_t rows, width;
+    float eps;
+} qw_rms_one_args;
+
+typedef struct {
+    uint16_t *qk;           /* [rows, ld]: q at col 0, k at col k_offset */
+    const uint16_t *norm_q; /* [128] */
+    const uint16_t *norm_k; /* [128] */
+    const float *rope_cos;  /* [rope_rows, 64] */
+    const float *rope_sin;
+    uint32_t rows, heads, ld, k_offset;
+    uint32_t rope_rows; /* table row = row % rope_rows (batched sequences) */
+    int32_t do_norm, do_rope;
+    float eps;
+} qw_qk_norm_rope_args;
+
+typedef struct {
+    uint16_t *out;
+    const uint16_t *residual;
+    const uint16_t *branch;
+    const uint16_t *modulation;
+    const uint32_t *row_map;
+    uint32_t rows, width, slots, gate_slot;
+} qw_gate_args;
+
+enum { QW_ACT_GELU_TANH = 0, QW_ACT_SILU = 1, QW_ACT_TANH = 2 };
+
+typedef struct {
+    uint16_t *out;
+    const uint16_t *in;
+    uint64_t count;
+    int32_t act;
+} qw_act_args;
+
+typedef struct {
+    uint16_t *out;     /* [rows, width] */
+    const uint16_t *fc1; /* [rows, 2 * width] = [gate | up] */
+    uint32_t rows, width;
+} qw_swiglu_args;
+
+typedef struct {
+    uint16_t *out;
+    const float *in;
+    uint64_t count;
+} qw_cast_args;
+
+typedef struct {
+    uint16_t *slots_out; /* [mod_rows, S * hidden] */
+    const uint16_t *raw;
+    uint32_t mod_rows, hidden;
+    int32_t shift_variant;
+} qw_reorder_args;
+
+typedef struct {
+    uint16_t *out;
+    uint64_t count;
+    uint64_t seed, stream;
+    float std, offset;
+} qw_fill_args;
+
+typedef struct {
+    int8_t *q;
+    float *scales;
+    const uint16_t *w;
+    uint32_t rows, cols;
+} qw_quant_args;
+
+typedef struct {
+    float *out;
+    const int8_t *q;
+    const float *scales;
+    uint32_t rows, cols;
+} qw_dequant_args;
+
+typedef struct {
+    void *dst;
+    const void *src;
+    uint64_t rows, row_bytes, dst_stride, src_stride; /* bytes */
+} qw_copy2d_args;
+
+/* Flash attention over a joint sequence: out[b*q_rows + r] attends keys
+ * [b*kv_rows, b*kv_rows + limit(r)) of the same batch entry. */
+typedef struct {
+    uint16_t *out;
+    const uint16_t *q;
+    const uint16_t *k;
+    const uint16_t *v;
+    const uint32_t *kv_limit; /* optional per-query-row limits [q_rows] */
+    uint32_t q_rows, kv_rows, heads;
+    uint32_t ldq, ldk, ldv, ldo; /* row strides in elements */
+    uint32_t text_rows;          /* closed-form limits when kv_limit == NULL */
+    int32_t text_causal;
+    float scale_log2; /* softmax scale * log2(e) */
+} qw_attn_args;
+
+#endif

@@ -1,0 +1,720 @@
+/* qwen_dit.c — C11 host of the DiT denoising forward over the HIP runtime.
+ *
+ * Follows the reference's qwen_dit.m (t2i path) call for call, with the
+ * MI355X layout changes:
+ *   - q|k|v come from ONE fused [rows, 3H] projection, per-head RMSNorm and
+ *     RoPE run fused in place on it, and attention reads q/k/v straight out
+ *     of it (no row-slice copies, qwen_dit.m:1373-1440);
+ *   - GELU is the up-projection's epilogue, the residual gate
+ *     (h += tanh(g) * branch) the down/out projections' epilogue, so the
+ *     branch tensor never round-trips HBM;
+ *   - the conditioning reorder runs on device (no submit + host round trip,
+ *     qwen_dit.m:1140-1186);
+ *   - CFG batch entries are stacked along rows: every linear sees
+ *     M = batch * rows, attention has a batch grid dimension.
+ * Rounding points are the reference kernels' (bf16 RNE at each reference
+ * op boundary). */
+#include "../../include/qwen_dit.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <strings.h>
+
+#include "../../include/qwen_gpu_ext.h"
+
+typedef struct {
+    h3_gpu_tensor *w;      /* bf16 or int8 [n, k] */
+    h3_gpu_tensor *scales; /* f32 [n] for int8 */
+    h3_gpu_tensor *bias;   /* bf16 [n] or NULL */
+    uint32_t n, k;
+} qw_lin;
+
+typedef struct {
+    qw_lin qkv, out, fc1, fc2;
+    h3_gpu_tensor *norm_q, *norm_k;
+} qw_layer;
+
+enum { P_EMBED, P_COND, P_INPUT, P_ATTN, P_OUT, P_LN, P_MLP, P_FINAL, P_COUNT };
+
+struct qw_dit {
+    h3_gpu *gpu;
+    qw_dit_config cfg;
+    qw_layer *layer;
+    qw_lin img_in, txt_in1, txt_in2, time_l1, time_l2, mod, norm_out, proj_out;
+    h3_gpu_tensor *txt_norm;
+    /* activation workspaces, sized for ws_rows rows */
+    uint32_t ws_rows;
+    h3_gpu_tensor *ws_mod, *ws_qkv, *ws_attn, *ws_wide, *ws_act;
+    uint32_t ws_text_rows;
+    h3_gpu_tensor *ws_tnorm, *ws_twide;
+    /* conditioning (2 modulation rows) */
+    h3_gpu_tensor *feat, *feat_bf16, *c_wide, *c_silu, *temb, *mod_raw,
+        *modulation, *norm_out_mod;
+    /* forward-owned joint sequence and row map */
+    uint32_t joint_rows;
+    h3_gpu_tensor *joint;
+    h3_gpu_tensor *row_map;
+    uint32_t rm_rows, rm_text, rm_batch;
+    int profile;
+    double prof_ms[P_COUNT];
+};
+
+static int set_error(char *error, size_t n, const char *fmt, ...) {
+    if (error && n) {
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(error, n, fmt, ap);
+        va_end(ap);
+    }
+    return 0;
+}
+
+static int env_on(const char *name) {
+    const char *v = getenv(name);
+    if (!v || !*v) return 0;
+    return strcmp(v, "0") && strcasecmp(v, "off") && strcasecmp(v, "false");
+}
+
+static uint32_t slots_of(const qw_dit_config *c) { return c->adaln_shift ? 6u : 4u; }
+
+void qw_dit_config_reference(qw_dit_config *c) {
+    memset(c, 0, sizeof(*c));
+    c->hidden = 4096;
+    c->heads = 32;
+    c->mlp_width = 12288;
+    c->text_dim = 4096;
+    c->z_dim = 64;
+    c->layers = 32;
+    c->mlp_act = QW_MLP_SWIGLU;
+    c->adaln_shift = 0;
+    c->has_bias = 0;
+    c->text_causal = 1;
+    c->int8_weights = 0;
+}
+
+void qw_dit_config_baseline(qw_dit_config *c) {
+    memset(c, 0, sizeof(*c));
+    c->hidden = 3072;
+    c->heads = 24;
+    c->mlp_width = 12288;
+    c->text_dim = 4096;
+    c->z_dim = 64;
+    c->layers = 32;
+    c->mlp_act = QW_MLP_GELU_TANH;
+    c->adaln_shift = 1;
+    c->has_bias = 1;
+    c->text_causal = 0;
+    c->int8_weights = 0;
+}
+
+qw_dit *qw_dit_create(h3_gpu *gpu, const char *model_dir, int layers, char *error,
+                      size_t error_size) {
+    (void)gpu;
+    (void)layers;
+    set_error(error, error_size,
+              "qw_dit_create(%s): loading released checkpoint shards is not part of this "
+              "build; use qw_dit_create_random",
+              model_dir ? model_dir : "(null)");
+    return NULL;
+}
+
+const qw_dit_config *qw_dit_get_config(const qw_dit *d) { return d ? &d->cfg : NULL; }
+
+/* ---------------------------------------------------------------------- */
+/* weights                                                                */
+
+static void lin_free(qw_lin *l) {
+    h3_gpu_tensor_free(l->w);
+    h3_gpu_tensor_free(l->scales);
+    h3_gpu_tensor_free(l->bias);
+    memset(l, 0, sizeof(*l));
+}
+
+/* W ~ bf16(0.02 z) from (seed, stream); int8 => quantised on device via the
+ * temporary bf16 tensor tmp (large enough for n * k). */
+static int lin_init(qw_dit *d, qw_lin *l, uint32_t n, uint32_t k, uint64_t seed,
+                    uint64_t stream, uint64_t bstream, int int8, h3_gpu_tensor *tmp) {
+    h3_gpu *g = d->gpu;
+    l->n = n;
+    l->k = k;
+    size_t count = (size_t)n * k;
+    if (int8) {
+        h3_gpu_tensor *view = h3_gpu_tensor_view(tmp, 0, count);
+        l->w = h3_gpu_tensor_new_i8(g, count);
+        l->scales = h3_gpu_tensor_new_f32(g, n);
+        int ok = view && l->w && l->scales &&
+                 qw_gpu_fill_normal_bf16(g, view, 0, count, seed, stream, 0.02f, 0.0f) &&
+                 h3_gpu_quantize_weight_int8(g, l->w, l->scales, view, n, k);
+        h3_gpu_tensor_free(view);
+        if (!ok) return 0;
+    } else {
+        l->w = h3_gpu_tensor_new_bf16(g, count);
+        if (!l->w || !qw_gpu_fill_normal_bf16(g, l->w, 0, count, seed, stream, 0.02f, 0.0f))
+            return 0;
+    }
+    if (d->cfg.has_bias) {
+        l->bias = h3_gpu_tensor_new_bf16(g, n);
+        if (!l->bias || !qw_gpu_fill_normal_bf16(g, l->bias, 0, n, seed, bstream, 0.02f, 0.0f))
+            return 0;
+    }
+    return 1;
+}
+
+static int check_config(const qw_dit_config *c, char *error, size_t n) {
+    if (!c) return set_error(error, n, "missing config");
+    if (!c->heads || c->hidden != c->heads * 128)
+        return set_error(error, n, "hidden %u must equal heads * 128", c->hidden);
+    if (c->hidden % 256 || c->hidden > 8192)
+        return set_error(error, n, "hidden %u must be a multiple of 256, <= 8192", c->hidden);
+    if (!c->mlp_width || c->mlp_width % 64)
+        return set_error(error, n, "mlp_width %u must be a multiple of 64", c->mlp_width);
+    if (!c->text_dim || c->text_dim % 64 || c->text_dim > 8192)
+        return set_error(error, n, "text_dim %u must be a multiple of 64, <= 8192", c->text_dim);
+    if (!c->z_dim || c->z_dim % 64)
+        return set_error(error, n, "z_dim %u must be a multiple of 64", c->z_dim);
+    if (!c->layers || c->layers > 256) return set_error(error, n, "layers %u out of range", c->layers);
+    if (c->mlp_act != QW_MLP_SWIGLU && c->mlp_act != QW_MLP_GELU_TANH)
+        return set_error(error, n, "unknown mlp_act %d", c->mlp_act);
+    return 1;
+}
+
+qw_dit *qw_dit_create_random(h3_gpu *gpu, const qw_dit_config *cfg, uint64_t seed,
+                             char *error, size_t error_size) {
+    if (!gpu) {
+        set_error(error, error_size, "no gpu");
+        return NULL;
+    }
+    if (!check_config(cfg, error, error_size)) return NULL;
+    qw_dit *d = calloc(1, sizeof(*d));
+    if (!d) {
+        set_error(error, error_size, "out of memory");
+        return NULL;
+    }
+    d->gpu = gpu;
+    d->cfg = *cfg;
+    d->profile = env_on("QWEN_BLOCK_PROFILE");
+    const uint32_t H = cfg->hidden, F = cfg->mlp_width;
+    const uint32_t f1 = cfg->mlp_act == QW_MLP_SWIGLU ? 2 * F : F;
+    const uint32_t nmod = slots_of(cfg) * H, nout = (cfg->adaln_shift ? 2 : 1) * H;
+    size_t tmp_n = (size_t)f1 * H;
+    if ((size_t)F * H > tmp_n) tmp_n = (size_t)F * H;
+    if ((size_t)3 * H * H > tmp_n) tmp_n = (size_t)3 * H * H;
+    h3_gpu_tensor *tmp = cfg->int8_weights ? h3_gpu_tensor_new_bf16(gpu, tmp_n) : NULL;
+    d->layer = calloc(cfg->layers, sizeof(qw_layer));
+    int ok = d->layer && (!cfg->int8_weights || tmp);
+    /* global projections stay bf16, as the reference keeps them */
+    ok = ok && lin_init(d, &d->img_in, H, cfg->z_dim, seed, QW_W_IMG_IN, QW_W_IMG_IN_B, 0, NULL);
+    d->txt_norm = ok ? h3_gpu_tensor_new_bf16(gpu, cfg->text_dim) : NULL;
+    ok = ok && d->txt_norm &&
+         qw_gpu_fill_normal_bf16(gpu, d->txt_norm, 0, cfg->text_dim, seed, QW_W_TXT_NORM, 0.02f,
+                                 0.0f);
+    ok = ok && lin_init(d, &d->txt_in1, H, cfg->text_dim, seed, QW_W_TXT_IN1, QW_W_TXT_IN1_B, 0, NULL);
+    ok = ok && lin_init(d, &d->txt_in2, H, H, seed, QW_W_TXT_IN2, QW_W_TXT_IN2_B, 0, NULL);
+    ok = ok && lin_init(d, &d->time_l1, H, 256, seed, QW_W_TIME_L1, QW_W_TIME_L1_B, 0, NULL);
+    ok = ok && lin_init(d, &d->time_l2, H, H, seed, QW_W_TIME_L2, QW_W_TIME_L2_B, 0, NULL);
+    ok = ok && lin_init(d, &d->mod, nmod, H, seed, QW_W_MOD, QW_W_MOD_B, 0, NULL);
+    ok = ok && lin_init(d, &d->norm_out, nout, H, seed, QW_W_NORM_OUT, QW_W_NORM_OUT_B, 0, NULL);
+    ok = ok && lin_init(d, &d->proj_out, cfg->z_dim, H, seed, QW_W_PROJ_OUT, QW_W_PROJ_OUT_B, 0, NULL);
+    for (uint32_t l = 0; ok && l < cfg->layers; l++) {
+        qw_layer *L = &d->layer[l];
+        int q8 = cfg->int8_weights;
+        ok = lin_init(d, &L->qkv, 3 * H, H, seed, QW_LAYER_STREAM(l, QW_L_QKV),
+                      QW_LAYER_STREAM(l, QW_L_QKV_B), q8, tmp) &&
+             lin_init(d, &L->out, H, H, seed, QW_LAYER_STREAM(l, QW_L_OUT),
+                      QW_LAYER_STREAM(l, QW_L_OUT_B), q8, tmp) &&
+             lin_init(d, &L->fc1, f1, H, seed, QW_LAYER_STREAM(l, QW_L_FC1),
+                      QW_LAYER_STREAM(l, QW_L_FC1_B), q8, tmp) &&
+             lin_init(d, &L->fc2, H, F, seed, QW_LAYER_STREAM(l, QW_L_FC2),
+                      QW_LAYER_STREAM(l, QW_L_FC2_B), q8, tmp);
+        L->norm_q = ok ? h3_gpu_tensor_new_bf16(gpu, 128) : NULL;
+        L->norm_k = ok ? h3_gpu_tensor_new_bf16(gpu, 128) : NULL;
+        ok = ok && L->norm_q && L->norm_k &&
+             qw_gpu_fill_normal_bf16(gpu, L->norm_q, 0, 128, seed, QW_LAYER_STREAM(l, QW_L_NORM_Q),
+                                     0.02f, 1.0f) &&
+             qw_gpu_fill_normal_bf16(gpu, L->norm_k, 0, 128, seed, QW_LAYER_STREAM(l, QW_L_NORM_K),
+                                     0.02f, 1.0f);
+    }
+    /* conditioning buffers (2 modulation rows) */
+    if (ok) {
+        d->feat = h3_gpu_tensor_new_f32(gpu, 2 * 256);
+        d->feat_bf16 = h3_gpu_tensor_new_bf16(gpu, 2 * 256);
+        d->c_wide = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)H);
+        d->c_silu = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)H);
+        d->temb = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)H);
+        d->mod_raw = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)nmod);
+        d->modulation = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)nmod);
+        d->norm_out_mod = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)nout);
+        ok = d->feat && d->feat_bf16 && d->c_wide && d->c_silu && d->temb && d->mod_raw &&
+             d->modulation && d->norm_out_mod;
+    }
+    ok = ok && h3_gpu_submit(gpu);
+    h3_gpu_tensor_free(tmp);
+    if (!ok) {
+        set_error(error, error_size, "qw_dit_create_random failed: %s", h3_gpu_error(gpu));
+        qw_dit_free(d);
+        return NULL;
+    }
+    return d;
+}
+
+void qw_dit_free(qw_dit *d) {
+    if (!d) return;
+    if (d->layer)
+        for (uint32_t l = 0; l < d->cfg.layers; l++) {
+            lin_free(&d->layer[l].qkv);
+            lin_free(&d->layer[l].out);
+            lin_free(&d->layer[l].fc1);
+            lin_free(&d->layer[l].fc2);
+            h3_gpu_tensor_free(d->layer[l].norm_q);
+            h3_gpu_tensor_free(d->layer[l].norm_k);
+        }
+    free(d->layer);
+    lin_free(&d->img_in);
+    lin_free(&d->txt_in1);
+    lin_free(&d->txt_in2);
+    lin_free(&d->time_l1);
+    lin_free(&d->time_l2);
+    lin_free(&d->mod);
+    lin_free(&d->norm_out);
+    lin_free(&d->proj_out);
+    h3_gpu_tensor *t[] = {d->txt_norm, d->ws_mod, d->ws_qkv, d->ws_attn, d->ws_wide, d->ws_act,
+                          d->ws_tnorm, d->ws_twide, d->feat, d->feat_bf16, d->c_wide, d->c_silu,
+                          d->temb, d->mod_raw, d->modulation, d->norm_out_mod, d->joint,
+                          d->row_map};
+    for (size_t i = 0; i < sizeof(t) / sizeof(t[0]); i++) h3_gpu_tensor_free(t[i]);
+    free(d);
+}
+
+const h3_gpu_tensor *qw_dit_block_tensor(const qw_dit *d, int block, int field) {
+    if (!d || block < 0 || (uint32_t)block >= d->cfg.layers) return NULL;
+    const qw_layer *L = &d->layer[block];
+    switch (field) {
+    case 0: case 1: case 2: return L->qkv.w;
+    case 3: return L->out.w;
+    case 4: return L->fc1.w;
+    case 5: return L->fc2.w;
+    default: return NULL;
+    }
+}
+
+const h3_gpu_tensor *qw_dit_block_scales(const qw_dit *d, int block, int field) {
+    if (!d || block < 0 || (uint32_t)block >= d->cfg.layers) return NULL;
+    const qw_layer *L = &d->layer[block];
+    switch (field) {
+    case 0: case 1: case 2: return L->qkv.scales;
+    case 3: return L->out.scales;
+    case 4: return L->fc1.scales;
+    case 5: return L->fc2.scales;
+    default: return NULL;
+    }
+}
+
+/* ---------------------------------------------------------------------- */
+/* helpers                                                                */
+
+static int linear(qw_dit *d, const qw_lin *l, h3_gpu_tensor *out, size_t out_off, uint32_t ldc,
+                  const h3_gpu_tensor *in, size_t in_off, uint32_t lda, uint32_t rows, int epi,
+                  const h3_gpu_tensor *modulation, const h3_gpu_tensor *row_map, uint32_t slots,
+                  uint32_t gate_slot) {
+    qw_linear_desc desc;
+    memset(&desc, 0, sizeof(desc));
+    desc.out = out;
+    desc.out_offset = out_off;
+    desc.ldc = ldc;
+    desc.in = in;
+    desc.in_offset = in_off;
+    desc.lda = lda;
+    desc.weight = l->w;
+    desc.wscale = l->scales;
+    desc.bias = l->bias;
+    desc.rows = rows;
+    desc.k = l->k;
+    desc.cols = l->n;
+    desc.epilogue = epi;
+    desc.modulation = modulation;
+    desc.row_map = row_map;
+    desc.slots = slots;
+    desc.gate_slot = gate_slot;
+    return qw_gpu_linear(d->gpu, &desc);
+}
+
+static int plain(qw_dit *d, const qw_lin *l, h3_gpu_tensor *out, const h3_gpu_tensor *in,
+                 uint32_t rows, int epi) {
+    return linear(d, l, out, 0, l->n, in, 0, l->k, rows, epi, NULL, NULL, 0, 0);
+}
+
+static void free_ws(qw_dit *d) {
+    h3_gpu_tensor_free(d->ws_mod);
+    h3_gpu_tensor_free(d->ws_qkv);
+    h3_gpu_tensor_free(d->ws_attn);
+    h3_gpu_tensor_free(d->ws_wide);
+    h3_gpu_tensor_free(d->ws_act);
+    d->ws_mod = d->ws_qkv = d->ws_attn = d->ws_wide = d->ws_act = NULL;
+    d->ws_rows = 0;
+}
+
+/* Block workspaces for `rows` rows (grow-only). */
+static int ensure_ws(qw_dit *d, uint32_t rows) {
+    if (d->ws_rows >= rows) return 1;
+    free_ws(d);
+    h3_gpu *g = d->gpu;
+    const size_t H = d->cfg.hidden, F = d->cfg.mlp_width;
+    const int swiglu = d->cfg.mlp_act == QW_MLP_SWIGLU;
+    d->ws_mod = h3_gpu_tensor_new_bf16(g, rows * H);
+    d->ws_qkv = h3_gpu_tensor_new_bf16(g, rows * 3 * H);
+    d->ws_attn = h3_gpu_tensor_new_bf16(g, rows * H);
+    d->ws_wide = h3_gpu_tensor_new_bf16(g, rows * (swiglu ? 2 * F : F));
+    d->ws_act = swiglu ? h3_gpu_tensor_new_bf16(g, rows * F) : NULL;
+    if (!d->ws_mod || !d->ws_qkv || !d->ws_attn || !d->ws_wide || (swiglu && !d->ws_act)) {
+        free_ws(d);
+        return 0;
+    }
+    d->ws_rows = rows;
+    return 1;
+}
+
+static int ensure_text_ws(qw_dit *d, uint32_t rows) {
+    if (d->ws_text_rows >= rows) return 1;
+    h3_gpu_tensor_free(d->ws_tnorm);
+    h3_gpu_tensor_free(d->ws_twide);
+    d->ws_tnorm = h3_gpu_tensor_new_bf16(d->gpu, (size_t)rows * d->cfg.text_dim);
+    d->ws_twide = h3_gpu_tensor_new_bf16(d->gpu, (size_t)rows * d->cfg.hidden);
+    d->ws_text_rows = d->ws_tnorm && d->ws_twide ? rows : 0;
+    return d->ws_text_rows != 0;
+}
+
+static void prof_begin(qw_dit *d) {
+    if (d->profile) h3_gpu_timer_begin(d->gpu);
+}
+
+static void prof_end(qw_dit *d, int stage) {
+    if (d->profile) {
+        double ms = h3_gpu_timer_end(d->gpu);
+        if (ms > 0) d->prof_ms[stage] += ms;
+    }
+}
+
+int qw_dit_block_profile(const qw_dit *d, double *ms, int max_stages) {
+    if (!d || !ms) return 0;
+    int n = max_stages < P_COUNT ? max_stages : P_COUNT;
+    for (int i = 0; i < n; i++) ms[i] = d->prof_ms[i];
+    return n;
+}
+
+/* ---------------------------------------------------------------------- */
+/* embed / conditioning                                                   */
+
+/* Text rows of one batch entry -> joint rows [joint_off, +text_rows):
+ * rms_norm_one -> txt_in1 (GELU epilogue) -> txt_in2 (qwen_dit.m:1031-1062). */
+static int embed_one(qw_dit *d, const h3_gpu_tensor *text_in, size_t text_off,
+                     uint32_t text_rows, const h3_gpu_tensor *latents, size_t lat_off,
+                     uint32_t image_rows, h3_gpu_tensor *joint, size_t joint_off) {
+    h3_gpu *g = d->gpu;
+    const uint32_t H = d->cfg.hidden;
+    if (text_rows) {
+        if (!ensure_text_ws(d, text_rows)) return 0;
+        h3_gpu_tensor *tv = h3_gpu_tensor_view(text_in, text_off, (size_t)text_rows * d->cfg.text_dim);
+        int ok = tv && qw_gpu_rms_norm_one_bf16(g, d->ws_tnorm, tv, d->txt_norm, text_rows,
+                                                d->cfg.text_dim, 1e-6f);
+        h3_gpu_tensor_free(tv);
+        ok = ok && plain(d, &d->txt_in1, d->ws_twide, d->ws_tnorm, text_rows, QW_LINEAR_GELU) &&
+             linear(d, &d->txt_in2, joint, joint_off, H, d->ws_twide, 0, H, text_rows,
+                    QW_LINEAR_STORE, NULL, NULL, 0, 0);
+        if (!ok) return 0;
+    }
+    if (image_rows)
+        return linear(d, &d->img_in, joint, joint_off + (size_t)text_rows * H, H, latents, lat_off,
+                      d->cfg.z_dim, image_rows, QW_LINEAR_STORE, NULL, NULL, 0, 0);
+    return 1;
+}
+
+int qw_dit_embed(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_rows,
+                 const h3_gpu_tensor *latents, uint32_t image_rows, h3_gpu_tensor *joint,
+                 char *error, size_t error_size) {
+    if (!d) return set_error(error, error_size, "no dit");
+    if (h3_gpu_tensor_elements(joint) < (size_t)(text_rows + image_rows) * d->cfg.hidden)
+        return set_error(error, error_size, "joint tensor too small");
+    if (text_rows && (!text_in || h3_gpu_tensor_elements(text_in) < (size_t)text_rows * d->cfg.text_dim))
+        return set_error(error, error_size, "text_in too small");
+    if (image_rows && (!latents || h3_gpu_tensor_elements(latents) < (size_t)image_rows * d->cfg.z_dim))
+        return set_error(error, error_size, "latents too small");
+    if (!embed_one(d, text_in, 0, text_rows, latents, 0, image_rows, joint, 0))
+        return set_error(error, error_size, "embed failed: %s", h3_gpu_error(d->gpu));
+    return 1;
+}
+
+void qw_dit_timestep_features(const float *row_sigmas, size_t count, float *features) {
+    /* qwen_dit.m:1085-1096: [cos(1000 s f_i) | sin(1000 s f_i)],
+     * f_i = 10000^(-i/128), computed in double, stored fp32. */
+    for (size_t r = 0; r < count; r++) {
+        const double t = (double)row_sigmas[r] * 1000.0;
+        for (int i = 0; i < 128; i++) {
+            const double arg = t * pow(10000.0, -(double)i / 128.0);
+            features[r * 256 + i] = (float)cos(arg);
+            features[r * 256 + 128 + i] = (float)sin(arg);
+        }
+    }
+}
+
+int qw_dit_conditioning(qw_dit *d, const h3_gpu_tensor *features, uint32_t mod_rows,
+                        h3_gpu_tensor *temb, h3_gpu_tensor *modulation,
+                        h3_gpu_tensor *norm_out_scale, char *error, size_t error_size) {
+    /* qwen_dit.m:1098-1192 */
+    if (!d) return set_error(error, error_size, "no dit");
+    h3_gpu *g = d->gpu;
+    const uint32_t H = d->cfg.hidden, S = slots_of(&d->cfg);
+    if (mod_rows == 0 || mod_rows > 2) return set_error(error, error_size, "mod_rows must be 1 or 2");
+    if (h3_gpu_tensor_elements(features) < (size_t)mod_rows * 256 ||
+        h3_gpu_tensor_elements(temb) < (size_t)mod_rows * H ||
+        h3_gpu_tensor_elements(modulation) < (size_t)mod_rows * S * H ||
+        h3_gpu_tensor_elements(norm_out_scale) < (size_t)mod_rows * d->norm_out.n)
+        return set_error(error, error_size, "conditioning tensors too small");
+    size_t n = (size_t)mod_rows * H;
+    int ok = h3_gpu_cast_f32_to_bf16(g, d->feat_bf16, features, mod_rows * 256) &&
+             plain(d, &d->time_l1, d->c_wide, d->feat_bf16, mod_rows, QW_LINEAR_STORE) &&
+             h3_gpu_silu_bf16(g, d->c_wide, d->c_wide, (uint32_t)n) &&
+             plain(d, &d->time_l2, temb, d->c_wide, mod_rows, QW_LINEAR_STORE) &&
+             h3_gpu_silu_bf16(g, d->c_silu, temb, (uint32_t)n) &&
+             plain(d, &d->norm_out, norm_out_scale, d->c_silu, mod_rows, QW_LINEAR_STORE) &&
+             plain(d, &d->mod, d->mod_raw, d->c_silu, mod_rows, QW_LINEAR_STORE) &&
+             qw_gpu_modulation_reorder_bf16(g, modulation, d->mod_raw, mod_rows, H,
+                                            d->cfg.adaln_shift);
+    if (!ok) return set_error(error, error_size, "conditioning failed: %s", h3_gpu_error(g));
+    return 1;
+}
+
+/* ---------------------------------------------------------------------- */
+/* block                                                                  */
+
+static int block_run(qw_dit *d, int li, h3_gpu_tensor *hidden, uint32_t batch, uint32_t rows,
+                     uint32_t text_rows, const h3_gpu_tensor *modulation,
+                     const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
+                     const h3_gpu_tensor *row_map, const h3_gpu_tensor *kv_limit,
+                     h3_gpu_tensor *k_out, h3_gpu_tensor *v_out, h3_gpu_tensor *debug_attn) {
+    h3_gpu *g = d->gpu;
+    const qw_layer *L = &d->layer[li];
+    const uint32_t H = d->cfg.hidden, F = d->cfg.mlp_width, S = slots_of(&d->cfg);
+    const uint32_t M = batch * rows;
+    const int sh = d->cfg.adaln_shift;
+    int ok;
+
+    prof_begin(d);
+    ok = qw_gpu_layer_norm_mod_shift_bf16(g, d->ws_mod, hidden, modulation, row_map, M, H, S, 0,
+                                          sh ? 4 : -1, 1e-6f) &&
+         plain(d, &L->qkv, d->ws_qkv, d->ws_mod, M, QW_LINEAR_STORE) &&
+         qw_gpu_qk_norm_rope_bf16(g, d->ws_qkv, M, d->cfg.heads, 3 * H, H, L->norm_q, L->norm_k,
+                                  rope_cos, rope_sin, rows, 1e-6f);
+    prof_end(d, P_INPUT);
+    if (!ok) return 0;
+
+    prof_begin(d);
+    qw_attention_desc ad;
+    memset(&ad, 0, sizeof(ad));
+    ad.out = d->ws_attn;
+    ad.ldo = H;
+    ad.q = ad.k = ad.v = d->ws_qkv;
+    ad.q_offset = 0;
+    ad.k_offset = H;
+    ad.v_offset = 2 * (size_t)H;
+    ad.ldq = ad.ldk = ad.ldv = 3 * H;
+    ad.kv_limit = kv_limit;
+    ad.batch = batch;
+    ad.q_rows = ad.kv_rows = rows;
+    ad.heads = d->cfg.heads;
+    ad.text_rows = text_rows;
+    ad.text_causal = d->cfg.text_causal;
+    ad.scale = 1.0f / sqrtf(128.0f);
+    ok = qw_gpu_attention_bf16(g, &ad);
+    if (ok && k_out) ok = qw_gpu_copy_rows(g, k_out, 0, H, d->ws_qkv, H, 3 * H, M, H);
+    if (ok && v_out) ok = qw_gpu_copy_rows(g, v_out, 0, H, d->ws_qkv, 2 * (size_t)H, 3 * H, M, H);
+    if (ok && debug_attn) ok = h3_gpu_copy_bf16(g, debug_attn, 0, d->ws_attn, 0, (size_t)M * H);
+    prof_end(d, P_ATTN);
+    if (!ok) return 0;
+
+    prof_begin(d);
+    ok = linear(d, &L->out, hidden, 0, H, d->ws_attn, 0, H, M, QW_LINEAR_GATE, modulation, row_map,
+                S, 2);
+    prof_end(d, P_OUT);
+    if (!ok) return 0;
+
+    prof_begin(d);
+    ok = qw_gpu_layer_norm_mod_shift_bf16(g, d->ws_mod, hidden, modulation, row_map, M, H, S, 1,
+                                          sh ? 5 : -1, 1e-6f);
+    prof_end(d, P_LN);
+    if (!ok) return 0;
+
+    prof_begin(d);
+    if (d->cfg.mlp_act == QW_MLP_GELU_TANH) {
+        ok = plain(d, &L->fc1, d->ws_wide, d->ws_mod, M, QW_LINEAR_GELU) &&
+             linear(d, &L->fc2, hidden, 0, H, d->ws_wide, 0, F, M, QW_LINEAR_GATE, modulation,
+                    row_map, S, 3);
+    } else {
+        ok = plain(d, &L->fc1, d->ws_wide, d->ws_mod, M, QW_LINEAR_STORE) &&
+             qw_gpu_swiglu_bf16(g, d->ws_act, d->ws_wide, M, F) &&
+             linear(d, &L->fc2, hidden, 0, H, d->ws_act, 0, F, M, QW_LINEAR_GATE, modulation,
+                    row_map, S, 3);
+    }
+    prof_end(d, P_MLP);
+    return ok;
+}
+
+static int check_row_map(const h3_gpu_tensor *row_map, uint32_t rows) {
+    return row_map && h3_gpu_tensor_dtype(row_map) == H3_GPU_U32 &&
+           h3_gpu_tensor_elements(row_map) >= rows;
+}
+
+int qw_dit_block(qw_dit *d, int layer, h3_gpu_tensor *hidden, const h3_gpu_tensor *modulation,
+                 const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
+                 const h3_gpu_tensor *row_map, uint32_t rows, uint32_t text_rows,
+                 const h3_gpu_tensor *kv_limit, const qw_dit_segment *segs, uint32_t seg_count,
+                 h3_gpu_tensor *k_out, h3_gpu_tensor *v_out, h3_gpu_tensor *debug_attn,
+                 char *error, size_t error_size) {
+    (void)segs;
+    (void)seg_count;
+    if (!d) return set_error(error, error_size, "no dit");
+    if (layer < 0 || (uint32_t)layer >= d->cfg.layers)
+        return set_error(error, error_size, "layer %d out of range", layer);
+    const size_t n = (size_t)rows * d->cfg.hidden;
+    if (text_rows > rows) return set_error(error, error_size, "text_rows > rows");
+    if (h3_gpu_tensor_elements(hidden) < n || !check_row_map(row_map, rows))
+        return set_error(error, error_size, "block %d: hidden/row_map too small", layer);
+    if ((k_out && h3_gpu_tensor_elements(k_out) < n) || (v_out && h3_gpu_tensor_elements(v_out) < n) ||
+        (debug_attn && h3_gpu_tensor_elements(debug_attn) < n))
+        return set_error(error, error_size, "block %d: output tensors too small", layer);
+    if (!ensure_ws(d, rows)) return set_error(error, error_size, "workspace allocation failed");
+    if (!block_run(d, layer, hidden, 1, rows, text_rows, modulation, rope_cos, rope_sin, row_map,
+                   kv_limit, k_out, v_out, debug_attn))
+        return set_error(error, error_size, "block %d kernel failed: %s", layer,
+                         h3_gpu_error(d->gpu));
+    return 1;
+}
+
+void qw_dit_prefix_limits(const qw_dit_segment *segs, uint32_t seg_count, uint32_t *limits) {
+    /* qwen_dit.m:1651-1665: text runs causal (run start + r + 1), image
+     * runs see every key up to their run end. */
+    uint32_t start = 0;
+    for (uint32_t s = 0; s < seg_count; s++) {
+        const uint32_t end = start + segs[s].rows;
+        for (uint32_t r = 0; r < segs[s].rows; r++)
+            limits[start + r] = segs[s].is_image ? end : start + r + 1;
+        start = end;
+    }
+}
+
+int qw_dit_final(qw_dit *d, h3_gpu_tensor *hidden, const h3_gpu_tensor *norm_out_scale,
+                 const h3_gpu_tensor *row_map, uint32_t rows, h3_gpu_tensor *output, char *error,
+                 size_t error_size) {
+    /* qwen_dit.m:1478-1496 */
+    if (!d) return set_error(error, error_size, "no dit");
+    const uint32_t H = d->cfg.hidden;
+    if (h3_gpu_tensor_elements(hidden) < (size_t)rows * H || !check_row_map(row_map, rows) ||
+        h3_gpu_tensor_elements(output) < (size_t)rows * d->cfg.z_dim)
+        return set_error(error, error_size, "final: tensors too small");
+    if (!ensure_ws(d, rows)) return set_error(error, error_size, "workspace allocation failed");
+    const int sh = d->cfg.adaln_shift;
+    int ok = qw_gpu_layer_norm_mod_shift_bf16(d->gpu, d->ws_mod, hidden, norm_out_scale, row_map,
+                                              rows, H, sh ? 2 : 1, 0, sh ? 1 : -1, 1e-6f) &&
+             plain(d, &d->proj_out, output, d->ws_mod, rows, QW_LINEAR_STORE);
+    if (!ok) return set_error(error, error_size, "final projection failed: %s", h3_gpu_error(d->gpu));
+    return 1;
+}
+
+/* ---------------------------------------------------------------------- */
+/* forward                                                                */
+
+static int ensure_row_map(qw_dit *d, uint32_t rows, uint32_t text_rows, uint32_t batch) {
+    if (d->row_map && d->rm_rows == rows && d->rm_text == text_rows && d->rm_batch == batch)
+        return 1;
+    h3_gpu_tensor_free(d->row_map);
+    d->row_map = NULL;
+    uint32_t *host = malloc(sizeof(uint32_t) * (size_t)rows * batch);
+    if (!host) return 0;
+    /* qwen_dit.m:1510-1516: text rows ride the t = 0 modulation row */
+    for (uint32_t b = 0; b < batch; b++)
+        for (uint32_t i = 0; i < rows; i++) host[(size_t)b * rows + i] = i < text_rows ? 1u : 0u;
+    d->row_map = h3_gpu_tensor_from_u32(d->gpu, host, (size_t)rows * batch);
+    free(host);
+    if (!d->row_map) return 0;
+    d->rm_rows = rows;
+    d->rm_text = text_rows;
+    d->rm_batch = batch;
+    return 1;
+}
+
+int qw_dit_forward_batch(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_rows,
+                         const h3_gpu_tensor *latents, uint32_t image_rows, uint32_t batch,
+                         float sigma, const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
+                         h3_gpu_tensor *output, char *error, size_t error_size) {
+    if (!d) return set_error(error, error_size, "no dit");
+    h3_gpu *g = d->gpu;
+    const uint32_t rows = text_rows + image_rows, H = d->cfg.hidden, S = slots_of(&d->cfg);
+    if (!batch || !rows) return set_error(error, error_size, "empty forward");
+    const uint32_t M = batch * rows;
+    if (text_rows && (!text_in || h3_gpu_tensor_elements(text_in) < (size_t)batch * text_rows * d->cfg.text_dim))
+        return set_error(error, error_size, "text_in too small");
+    if (image_rows && (!latents || h3_gpu_tensor_elements(latents) < (size_t)batch * image_rows * d->cfg.z_dim))
+        return set_error(error, error_size, "latents too small");
+    if (!output || h3_gpu_tensor_elements(output) < (size_t)M * d->cfg.z_dim)
+        return set_error(error, error_size, "output too small");
+    if (!rope_cos || !rope_sin || h3_gpu_tensor_elements(rope_cos) < (size_t)rows * 64 ||
+        h3_gpu_tensor_elements(rope_sin) < (size_t)rows * 64)
+        return set_error(error, error_size, "rope tables must cover %u rows", rows);
+    if (!ensure_ws(d, M) || !ensure_row_map(d, rows, text_rows, batch))
+        return set_error(error, error_size, "forward allocation failed: %s", h3_gpu_error(g));
+    if (d->joint_rows < M) {
+        h3_gpu_tensor_free(d->joint);
+        d->joint = h3_gpu_tensor_new_bf16(g, (size_t)M * H);
+        d->joint_rows = d->joint ? M : 0;
+        if (!d->joint) return set_error(error, error_size, "joint allocation failed");
+    }
+    if (d->profile) memset(d->prof_ms, 0, sizeof(d->prof_ms));
+
+    prof_begin(d);
+    for (uint32_t b = 0; b < batch; b++)
+        if (!embed_one(d, text_in, (size_t)b * text_rows * d->cfg.text_dim, text_rows, latents,
+                       (size_t)b * image_rows * d->cfg.z_dim, image_rows, d->joint,
+                       (size_t)b * rows * H))
+            return set_error(error, error_size, "embed failed: %s", h3_gpu_error(g));
+    prof_end(d, P_EMBED);
+
+    prof_begin(d);
+    const float sigmas[2] = {sigma, 0.0f};
+    float feats[512];
+    qw_dit_timestep_features(sigmas, 2, feats);
+    if (!h3_gpu_tensor_write_f32(d->feat, feats, 512) ||
+        !qw_dit_conditioning(d, d->feat, 2, d->temb, d->modulation, d->norm_out_mod, error,
+                             error_size))
+        return error && *error ? 0 : set_error(error, error_size, "conditioning failed");
+    prof_end(d, P_COND);
+
+    for (uint32_t l = 0; l < d->cfg.layers; l++)
+        if (!block_run(d, (int)l, d->joint, batch, rows, text_rows, d->modulation, rope_cos,
+                       rope_sin, d->row_map, NULL, NULL, NULL, NULL))
+            return set_error(error, error_size, "block %u kernel failed: %s", l, h3_gpu_error(g));
+
+    prof_begin(d);
+    const int sh = d->cfg.adaln_shift;
+    int ok = qw_gpu_layer_norm_mod_shift_bf16(g, d->ws_mod, d->joint, d->norm_out_mod, d->row_map,
+                                              M, H, sh ? 2 : 1, 0, sh ? 1 : -1, 1e-6f) &&
+             plain(d, &d->proj_out, output, d->ws_mod, M, QW_LINEAR_STORE);
+    prof_end(d, P_FINAL);
+    (void)S;
+    if (!ok) return set_error(error, error_size, "final projection failed: %s", h3_gpu_error(g));
+    return 1;
+}
+
+int qw_dit_forward(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_rows,
+                   const h3_gpu_tensor *latents, uint32_t image_rows, float sigma,
+                   const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
+                   h3_gpu_tensor *output, char *error, size_t error_size) {
+    /* qwen_dit.m:1498-1568 (the reference submits inside; so do we, at the
+     * end, so the caller's read sees the result) */
+    return qw_dit_forward_batch(d, text_in, text_rows, latents, image_rows, 1, sigma, rope_cos,
+                                rope_sin, output, error, error_size) &&
+           (h3_gpu_submit(d->gpu) && h3_gpu_begin(d->gpu)
+                ? 1
+                : set_error(error, error_size, "forward failed: %s", h3_gpu_error(d->gpu)));
+}

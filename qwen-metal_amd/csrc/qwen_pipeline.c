@@ -1,0 +1,249 @@
+/* qwen_pipeline.c — scheduler, joint RoPE tables and the FlowMatch Euler
+ * denoise loop around the DiT forward (reference qwen_pipeline.m:130-486).
+ * With guidance, the cond and uncond branches run as one batch-2 forward
+ * (M = 2 * rows in every linear) when their text lengths match. */
+#include "../../include/qwen_pipeline.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+void qw_sched_cfg_default(qw_sched_cfg *c) {
+    c->dynamic_shifting = 1;
+    c->base_seq = 256.0;
+    c->max_seq = 8192.0;
+    c->base_shift = 0.5;
+    c->max_shift = 0.9;
+    c->has_terminal = 1;
+    c->shift_terminal = 0.02;
+}
+
+static float f32(double v) { return (float)v; }
+
+int qw_pipe_schedule(uint32_t steps, uint32_t seq_len, const double *turbo_sigmas,
+                     uint32_t turbo_count, const qw_sched_cfg *cfg, double *sigmas_out,
+                     char *error, size_t error_size) {
+    /* qwen_pipeline.m:130-205: float32 intermediates, exp(mu) in double. */
+    if (!steps || !seq_len || !sigmas_out || !cfg || steps > 1000) {
+        snprintf(error, error_size, "schedule: bad arguments");
+        return 0;
+    }
+    if (turbo_sigmas && turbo_count != steps) {
+        snprintf(error, error_size, "schedule: turbo sigmas %u != steps %u", turbo_count, steps);
+        return 0;
+    }
+    double exp_mu = 0.0;
+    if (cfg->dynamic_shifting) {
+        double m = cfg->max_seq != cfg->base_seq
+                       ? (cfg->max_shift - cfg->base_shift) / (cfg->max_seq - cfg->base_seq)
+                       : 0.0;
+        double b = cfg->base_shift - m * cfg->base_seq;
+        exp_mu = exp((double)seq_len * m + b);
+    }
+    float *sh = malloc(sizeof(float) * steps);
+    if (!sh) {
+        snprintf(error, error_size, "schedule: out of memory");
+        return 0;
+    }
+    for (uint32_t i = 0; i < steps; i++) {
+        double raw = turbo_sigmas ? turbo_sigmas[i]
+                     : steps == 1 ? 1.0
+                                  : 1.0 + (double)i * ((1.0 / steps) - 1.0) / (double)(steps - 1);
+        float t = f32(raw);
+        if (cfg->dynamic_shifting) {
+            float inv = f32(1.0 / t);
+            float base = f32(inv - 1.0f);
+            sh[i] = f32(exp_mu / (exp_mu + (double)base));
+        } else {
+            sh[i] = f32(raw);
+        }
+    }
+    if (cfg->has_terminal && cfg->shift_terminal < 1.0) {
+        float tail = f32(1.0 - (double)sh[steps - 1]);
+        float scale = f32((double)tail / (1.0 - cfg->shift_terminal));
+        if (scale != 0.0f)
+            for (uint32_t i = 0; i < steps; i++) {
+                float om = f32(1.0 - (double)sh[i]);
+                sh[i] = f32(1.0 - (double)om / (double)scale);
+            }
+    }
+    for (uint32_t i = 0; i < steps; i++) sigmas_out[i] = sh[i];
+    sigmas_out[steps] = 0.0;
+    free(sh);
+    return 1;
+}
+
+void qw_pipe_rope_tables_host(uint32_t text_rows, uint32_t gh, uint32_t gw, float *cos_out,
+                              float *sin_out) {
+    /* qwen_pipeline.m:212-273: axes (16, 56, 56), text row t at (t, t, t),
+     * image row (h, w) at (text_rows, h - ceil(gh/2), w - ceil(gw/2)). */
+    static const int dims[3] = {16, 56, 56};
+    const uint32_t rows = text_rows + gh * gw;
+    const long ch = (long)(gh - gh / 2), cw = (long)(gw - gw / 2);
+    for (uint32_t t = 0; t < rows; t++) {
+        double pos[3];
+        if (t < text_rows) {
+            pos[0] = pos[1] = pos[2] = (double)t;
+        } else {
+            const uint32_t idx = t - text_rows;
+            pos[0] = (double)text_rows;
+            pos[1] = (double)((long)(idx / gw) - ch);
+            pos[2] = (double)((long)(idx % gw) - cw);
+        }
+        size_t col = (size_t)t * 64;
+        for (int a = 0; a < 3; a++)
+            for (int p = 0; p < dims[a] / 2; p++, col++) {
+                const double ang = pos[a] * pow(10000.0, -2.0 * (double)p / (double)dims[a]);
+                cos_out[col] = (float)cos(ang);
+                sin_out[col] = (float)sin(ang);
+            }
+    }
+}
+
+int qw_pipe_rope_tables(h3_gpu *gpu, uint32_t text_rows, uint32_t gh, uint32_t gw,
+                        h3_gpu_tensor **rope_cos, h3_gpu_tensor **rope_sin, char *error,
+                        size_t error_size) {
+    if (!gh || !gw || !rope_cos || !rope_sin) {
+        snprintf(error, error_size, "rope: bad arguments");
+        return 0;
+    }
+    const size_t n = (size_t)(text_rows + gh * gw) * 64;
+    float *c = malloc(sizeof(float) * n), *s = malloc(sizeof(float) * n);
+    h3_gpu_tensor *ct = NULL, *st = NULL;
+    int ok = c && s;
+    if (ok) {
+        qw_pipe_rope_tables_host(text_rows, gh, gw, c, s);
+        ct = h3_gpu_tensor_from_f32(gpu, c, n);
+        st = h3_gpu_tensor_from_f32(gpu, s, n);
+        ok = ct && st;
+    }
+    free(c);
+    free(s);
+    if (!ok) {
+        h3_gpu_tensor_free(ct);
+        h3_gpu_tensor_free(st);
+        snprintf(error, error_size, "rope: table build failed");
+        return 0;
+    }
+    *rope_cos = ct;
+    *rope_sin = st;
+    return 1;
+}
+
+static uint16_t bf16_rne(float v) {
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+static float bf16_f32(uint16_t v) {
+    uint32_t b = (uint32_t)v << 16;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+int qw_pipe_denoise(qw_dit *dit, h3_gpu *gpu, const h3_gpu_tensor *text_in, uint32_t text_rows,
+                    const h3_gpu_tensor *neg_text_in, uint32_t neg_rows, float *latents,
+                    uint32_t gh, uint32_t gw, uint32_t steps, float cfg_scale,
+                    const double *turbo_sigmas, uint32_t turbo_count, const qw_sched_cfg *sched,
+                    char *error, size_t error_size) {
+    /* qwen_pipeline.m:289-486 */
+    const qw_dit_config *cfg = qw_dit_get_config(dit);
+    if (!cfg || !gpu || !latents || !gh || !gw || !steps) {
+        snprintf(error, error_size, "denoise: bad arguments");
+        return 0;
+    }
+    const uint32_t z = cfg->z_dim, image_rows = gh * gw;
+    const size_t count = (size_t)image_rows * z;
+    const int guided = cfg_scale > 1.0f && neg_text_in && neg_rows;
+    const int stacked = guided && neg_rows == text_rows;
+    const uint32_t rows = text_rows + image_rows, nrows = neg_rows + image_rows;
+    double *sigmas = malloc(sizeof(double) * (steps + 1));
+    uint16_t *lat_host = malloc(sizeof(uint16_t) * count * 2);
+    uint16_t *pred_host = malloc(sizeof(uint16_t) * (size_t)(rows + (guided ? nrows : 0)) * z);
+    h3_gpu_tensor *cos_t = NULL, *sin_t = NULL, *ncos = NULL, *nsin = NULL;
+    h3_gpu_tensor *lat = NULL, *pred = NULL, *npred = NULL, *text2 = NULL;
+    int ok = sigmas && lat_host && pred_host;
+    if (!ok) {
+        snprintf(error, error_size, "denoise: out of memory");
+        goto done;
+    }
+    ok = qw_pipe_schedule(steps, image_rows, turbo_sigmas, turbo_count, sched, sigmas, error,
+                          error_size) &&
+         qw_pipe_rope_tables(gpu, text_rows, gh, gw, &cos_t, &sin_t, error, error_size);
+    if (ok && guided && !stacked)
+        ok = qw_pipe_rope_tables(gpu, neg_rows, gh, gw, &ncos, &nsin, error, error_size);
+    if (!ok) goto done;
+    lat = h3_gpu_tensor_new_bf16(gpu, count * (stacked ? 2 : 1));
+    pred = h3_gpu_tensor_new_bf16(gpu, (size_t)rows * z * (stacked ? 2 : 1));
+    if (guided && !stacked) npred = h3_gpu_tensor_new_bf16(gpu, (size_t)nrows * z);
+    if (stacked && text_rows) {
+        /* [cond text; uncond text] stacked for the batch-2 forward */
+        text2 = h3_gpu_tensor_new_bf16(gpu, (size_t)2 * text_rows * cfg->text_dim);
+        ok = text2 &&
+             h3_gpu_copy_bf16(gpu, text2, 0, text_in, 0, (size_t)text_rows * cfg->text_dim) &&
+             h3_gpu_copy_bf16(gpu, text2, (size_t)text_rows * cfg->text_dim, neg_text_in, 0,
+                              (size_t)text_rows * cfg->text_dim);
+    }
+    ok = ok && lat && pred && (!guided || stacked || npred);
+    if (!ok) {
+        snprintf(error, error_size, "denoise: allocation failed: %s", h3_gpu_error(gpu));
+        goto done;
+    }
+    h3_gpu_begin(gpu);
+    for (uint32_t step = 0; ok && step < steps; step++) {
+        for (size_t i = 0; i < count; i++) lat_host[i] = bf16_rne(latents[i]);
+        if (stacked) memcpy(lat_host + count, lat_host, sizeof(uint16_t) * count);
+        const float sigma = (float)sigmas[step];
+        ok = h3_gpu_tensor_write_bf16(lat, lat_host, count * (stacked ? 2 : 1));
+        if (ok && stacked) {
+            ok = qw_dit_forward_batch(dit, text_rows ? text2 : NULL, text_rows, lat, image_rows, 2,
+                                      sigma, cos_t, sin_t, pred, error, error_size) &&
+                 h3_gpu_submit(gpu) && h3_gpu_begin(gpu) &&
+                 h3_gpu_tensor_read_bf16(pred, pred_host, (size_t)2 * rows * z);
+        } else if (ok) {
+            ok = qw_dit_forward(dit, text_in, text_rows, lat, image_rows, sigma, cos_t, sin_t, pred,
+                                error, error_size) &&
+                 h3_gpu_tensor_read_bf16(pred, pred_host, (size_t)rows * z);
+            if (ok && guided)
+                ok = qw_dit_forward(dit, neg_text_in, neg_rows, lat, image_rows, sigma, ncos, nsin,
+                                    npred, error, error_size) &&
+                     h3_gpu_tensor_read_bf16(npred, pred_host + (size_t)rows * z,
+                                             (size_t)nrows * z);
+        }
+        if (!ok) {
+            if (error && !*error) snprintf(error, error_size, "denoise step %u: %s", step,
+                                           h3_gpu_error(gpu));
+            break;
+        }
+        /* x += (sigma_next - sigma) * (neg + cfg (pos - neg)), fp32 on host */
+        const float dt = (float)(sigmas[step + 1] - sigmas[step]);
+        const uint16_t *pos = pred_host + (size_t)text_rows * z;
+        const uint16_t *neg =
+            pred_host + (size_t)rows * z + (size_t)(stacked ? text_rows : neg_rows) * z;
+        for (size_t i = 0; i < count; i++) {
+            float p = bf16_f32(pos[i]);
+            if (guided) {
+                float n = bf16_f32(neg[i]);
+                p = n + cfg_scale * (p - n);
+            }
+            latents[i] += dt * p;
+        }
+    }
+done:
+    h3_gpu_tensor_free(cos_t);
+    h3_gpu_tensor_free(sin_t);
+    h3_gpu_tensor_free(ncos);
+    h3_gpu_tensor_free(nsin);
+    h3_gpu_tensor_free(lat);
+    h3_gpu_tensor_free(pred);
+    h3_gpu_tensor_free(npred);
+    h3_gpu_tensor_free(text2);
+    free(sigmas);
+    free(lat_host);
+    free(pred_host);
+    return ok;
+}

@@ -46,3 +46,33 @@ def oracle():
     from oracle import oracle as o
     o.lib()
     return o
+
+
+def load_qdit():
+    """The product's ctypes binding (qwen-metal_amd/qdit.py)."""
+    import importlib.util
+    path = os.path.join(ROOT, "qwen-metal_amd", "qdit.py")
+    spec = importlib.util.spec_from_file_location("qdit", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+@pytest.fixture(scope="session")
+def qd():
+    return load_qdit()
+
+
+@pytest.fixture(scope="session")
+def gpu(qd):
+    g = qd.Gpu()
+    yield g
+    g.close()
+
+
+def ulp_diff(a, b):
+    """Distance in bf16 units between two bf16 bit arrays (sign-aware)."""
+    def key(x):
+        x = np.asarray(x, np.int32)
+        return np.where(x & 0x8000, 0x8000 - (x & 0x7FFF), 0x8000 + (x & 0x7FFF))
+    return np.abs(key(a) - key(b))

@@ -1,0 +1,165 @@
+"""The DiT block and forward on the GPU, through the C-ABI
+(qwen_dit.h), against the oracle with the SAME seeded weights (the
+library and the oracle derive every weight from the counter-based
+generator; int8 weights are checked bit-exact first).
+
+Bounds (north_star): per block cosine >= 0.9999 and relL2 within the
+bf16 noise band; the velocity after the full depth relL2 <= 1e-2."""
+import numpy as np
+import pytest
+
+from conftest import cosine, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(hidden=256, heads=2, mlp_width=512, text_dim=256, z_dim=64, layers=3)
+
+
+def cfg(base, **kw):
+    c = dict(SMALL if base == "small" else {})
+    c.update(kw)
+    return c
+
+
+REF_VARIANT = dict(mlp_act=0, adaln_shift=0, has_bias=0, text_causal=1)
+BASE_VARIANT = dict(mlp_act=1, adaln_shift=1, has_bias=1, text_causal=0)
+
+
+def _inputs(oracle, c, batch, text_rows, gh, gw, seed):
+    I = gh * gw
+    text = oracle.fill_normal_bf16(batch * text_rows * c["text_dim"], seed, 900)
+    lat = oracle.fill_normal_bf16(batch * I * c["z_dim"], seed, 901)
+    cos, sin = oracle.rope_tables(text_rows, gh, gw)
+    return text, lat, cos, sin
+
+
+def _run_forward(gpu, qd, oracle, c, batch, text_rows, gh, gw, sigma, seed=7):
+    I = gh * gw
+    R = text_rows + I
+    text, lat, cos, sin = _inputs(oracle, c, batch, text_rows, gh, gw, seed)
+    dit = qd.Dit(gpu, c, seed)
+    out = gpu.new(batch * R * c["z_dim"], qd.BF16)
+    dit.forward_batch(gpu.put(text) if text_rows else None, text_rows, gpu.put(lat), I, batch,
+                      sigma, gpu.put(cos), gpu.put(sin), out)
+    gpu.submit()
+    got = out.read().reshape(batch, R, c["z_dim"])
+    om = oracle.Model(c, seed, c["layers"])
+    refs = []
+    for b in range(batch):
+        t = text[b * text_rows * c["text_dim"]:(b + 1) * text_rows * c["text_dim"]].copy()
+        l_ = lat[b * I * c["z_dim"]:(b + 1) * I * c["z_dim"]].copy()
+        refs.append(om.forward(t, text_rows, l_, I, sigma, cos, sin, c["layers"]))
+    om.close()
+    dit.close()
+    return got, np.stack(refs)
+
+
+@pytest.mark.parametrize("variant", [REF_VARIANT, BASE_VARIANT], ids=["ref", "baseline"])
+@pytest.mark.parametrize("int8", [0, 1])
+def test_forward_small(gpu, qd, oracle, variant, int8):
+    c = cfg("small", int8_weights=int8, **variant)
+    got, ref = _run_forward(gpu, qd, oracle, c, 2, 16, 8, 8, 0.37)
+    f = oracle.bf16_to_f32
+    for b in range(2):
+        assert rel_l2(f(got[b]), f(ref[b])) < 1e-2
+        assert cosine(f(got[b]), f(ref[b])) > 0.9999
+
+
+def test_forward_no_text_rows(gpu, qd, oracle):
+    """dit_fixture case a topology: image rows only."""
+    c = cfg("small", **REF_VARIANT)
+    got, ref = _run_forward(gpu, qd, oracle, c, 1, 0, 4, 4, 0.37)
+    f = oracle.bf16_to_f32
+    assert rel_l2(f(got), f(ref)) < 1e-2
+
+
+def test_int8_weights_bit_exact(gpu, qd, oracle):
+    """The library's device-quantised block weights equal the oracle's
+    quantisation of the same seeded bf16 weights, bit for bit."""
+    c = cfg("small", int8_weights=1, **BASE_VARIANT)
+    dit = qd.Dit(gpu, c, 99)
+    om = oracle.Model(c, 99, c["layers"])
+    import ctypes as C
+    for layer in range(c["layers"]):
+        L = om.m.layer[layer]
+        for field, lin in ((0, L.qkv), (3, L.out), (4, L.fc1), (5, L.fc2)):
+            n, k = lin.n, lin.k
+            wt = qd.Tensor(gpu, dit.block_tensor(layer, field), n * k, qd.I8, owner=dit)
+            st = qd.Tensor(gpu, qd.lib().qw_dit_block_scales(dit.h, layer, field), n, qd.F32,
+                           owner=dit)
+            q_ref = np.ctypeslib.as_array(C.cast(lin.q, C.POINTER(C.c_int8)), (n * k,))
+            s_ref = np.ctypeslib.as_array(lin.scales, (n,))
+            assert np.array_equal(wt.read(), q_ref)
+            assert np.array_equal(st.read(), s_ref)
+            wt.h = st.h = None  # borrowed handles
+    om.close()
+    dit.close()
+
+
+@pytest.mark.parametrize("variant", [REF_VARIANT, BASE_VARIANT], ids=["ref", "baseline"])
+def test_block_api_matches_oracle(gpu, qd, oracle, variant):
+    """qw_dit_block (reference signature) on a caller-owned hidden state,
+    with debug_attn and K/V export, against qo_block."""
+    c = cfg("small", **variant)
+    H, S = c["hidden"], 6 if c["adaln_shift"] else 4
+    T, gh, gw = 8, 3, 4
+    R = T + gh * gw
+    hid = oracle.fill_normal_bf16(R * H, 5, 950)
+    mod = oracle.fill_normal_bf16(2 * S * H, 5, 951, 0.2)
+    rm = (np.arange(R) < T).astype(np.uint32)
+    cos, sin = oracle.rope_tables(T, gh, gw)
+    dit = qd.Dit(gpu, c, 3)
+    ht = gpu.put(hid)
+    dbg, ko, vo = (gpu.new(R * H, qd.BF16) for _ in range(3))
+    dit.block(1, ht, gpu.put(mod), gpu.put(cos), gpu.put(sin), gpu.put(rm), R, T,
+              k_out=ko, v_out=vo, debug_attn=dbg)
+    gpu.submit()
+    om = oracle.Model(c, 3, c["layers"])
+    ref_h = hid.copy()
+    ref_attn = om.block(1, ref_h, mod, cos, sin, rm, R, T, want_attn=True)
+    f = oracle.bf16_to_f32
+    assert cosine(f(dbg.read()), f(ref_attn)) > 0.9999
+    assert rel_l2(f(ht.read()), f(ref_h)) < 1e-2
+    assert cosine(f(ht.read()), f(ref_h)) > 0.9999
+    assert np.any(ko.read() != 0) and np.any(vo.read() != 0)
+    om.close()
+    dit.close()
+
+
+def test_block_prefix_limits(gpu, qd, oracle):
+    """kv_limit path (ti2i prefix table, qwen_dit.h:141-145) through
+    qw_dit_block against qo_block with the same limits."""
+    import ctypes as C
+    c = cfg("small", **REF_VARIANT)
+    H = c["hidden"]
+    segs = [(20, 0), (48, 1), (17, 0), (64, 1)]
+    R = sum(r for r, _ in segs)
+
+    class Seg(C.Structure):
+        _fields_ = [("rows", C.c_uint32), ("is_image", C.c_int), ("src_offset", C.c_uint32)]
+    arr = (Seg * len(segs))(*[Seg(r, i, 0) for r, i in segs])
+    lim = np.empty(R, np.uint32)
+    qd.lib().qw_dit_prefix_limits(arr, len(segs), lim.ctypes.data)
+    assert lim[0] == 1 and lim[19] == 20 and lim[20] == 68 and lim[68] == 69 and lim[-1] == R
+    hid = oracle.fill_normal_bf16(R * H, 6, 960)
+    mod = oracle.fill_normal_bf16(2 * 4 * H, 6, 961, 0.2)
+    rm = np.zeros(R, np.uint32)
+    cos, sin = oracle.rope_tables(0, 1, R)
+    dit = qd.Dit(gpu, c, 4)
+    ht = gpu.put(hid)
+    dit.block(0, ht, gpu.put(mod), gpu.put(cos), gpu.put(sin), gpu.put(rm), R, 0,
+              kv_limit=gpu.put(lim))
+    gpu.submit()
+    om = oracle.Model(c, 4, 1)
+    ref = hid.copy()
+    om.block(0, ref, mod, cos, sin, rm, R, 0, limits=lim)
+    f = oracle.bf16_to_f32
+    assert rel_l2(f(ht.read()), f(ref)) < 1e-2
+    om.close()
+    dit.close()
+
+
+@pytest.fixture(autouse=True)
+def _release_uploads(gpu):
+    yield
+    gpu.release()
