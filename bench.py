@@ -1,0 +1,223 @@
+#!/usr/bin/env python3
+"""DiT denoise-step benchmark on one MI355X.
+
+Workload: one 1024x1024 denoise step of the
+32-layer DiT with classifier-free guidance as ONE batch-2 forward
+(cond + uncond stacked, 4096 image + 256 text tokens each, M = 8704 rows in
+every linear), hidden 3072, 24 x 128 heads, GELU-tanh MLP 12288,
+shift/scale/gate adaLN, biases, int8 weight-only block linears with fp32
+per-output-channel scales, bf16 activations, fp32 softmax. Weights and
+inputs are seeded synthetic data generated on the device (no checkpoint).
+
+Timed region: K forward steps (embed, conditioning, 32 blocks, final head)
+with every input already resident in HBM, bracketed by a device sync and
+hipEvents on the library's stream. The dominant kernel (the int8-weight
+up-projection GEMM, M=8704 K=3072 N=12288, GELU epilogue) is timed the same
+way, on the same stream, for the roofline entry; every other linear shape
+and the attention kernel are timed alongside for the breakdown.
+
+cpu_baseline: the CPU oracle (oracle/, OpenMP) runs ONE of the 32 blocks for
+ONE of the 2 CFG branches at the full 4352-row shape, scaled x64 to a step.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+CFG = dict(hidden=3072, heads=24, mlp_width=12288, text_dim=4096, z_dim=64, layers=32,
+           mlp_act=1, adaln_shift=1, has_bias=1, text_causal=0, int8_weights=1)
+TEXT, GH, GW, BATCH, SIGMA, SEED = 256, 64, 64, 2, 0.5, 2026
+
+
+def load_qdit():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "qdit", os.path.join(ROOT, "qwen-metal_amd", "qdit.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def flops(cfg, rows, text_rows, batch):
+    H, F, heads = cfg["hidden"], cfg["mlp_width"], cfg["heads"]
+    f1 = 2 * F if cfg["mlp_act"] == 0 else F
+    per_row = 3 * H * H + H * H + f1 * H + F * H
+    lin = 2.0 * rows * per_row * cfg["layers"] * batch
+    image = rows - text_rows
+    text_keys = text_rows * (text_rows + 1) // 2 if cfg["text_causal"] else text_rows * text_rows
+    visible = text_keys + image * rows
+    sdpa = 4.0 * 128 * heads * visible * cfg["layers"] * batch
+    extra = 2.0 * batch * (text_rows * (cfg["text_dim"] * H + H * H) + image * cfg["z_dim"] * H +
+                           rows * H * cfg["z_dim"])
+    return lin, sdpa, extra
+
+
+def time_ms(gpu, fn, reps):
+    gpu.submit()
+    gpu.timer_begin()
+    for _ in range(reps):
+        fn()
+    return gpu.timer_end() / reps
+
+
+def kernel_breakdown(qd, gpu, reps=10):
+    """Each linear shape of the step and the attention kernel, alone."""
+    H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
+    L = qd.lib()
+    a = gpu.new(M * F, qd.BF16)
+    out = gpu.new(M * 3 * H, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, a.h, 0, M * F, 1, 1, 1.0, 0.0), "fill")
+    shapes = {"qkv": (H, 3 * H, qd.LINEAR_STORE), "out": (H, H, qd.LINEAR_STORE),
+              "up": (H, F, qd.LINEAR_GELU), "down": (F, H, qd.LINEAR_STORE)}
+    res = {}
+    for name, (k, n, epi) in shapes.items():
+        wb = gpu.new(n * k, qd.BF16)
+        q = gpu.new(n * k, qd.I8)
+        s = gpu.new(n, qd.F32)
+        gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, wb.h, 0, n * k, 1, 2, 0.02, 0.0), "fill")
+        gpu.check(L.h3_gpu_quantize_weight_int8(gpu.h, q.h, s.h, wb.h, n, k), "quant")
+        big = gpu.new(M * n, qd.BF16) if n > 3 * H else out
+        run = lambda: gpu.linear(big, a, q, M, k, n, wscale=s, epilogue=epi)  # noqa: E731
+        run()
+        ms = time_ms(gpu, run, reps)
+        fl = 2.0 * M * n * k
+        res[name] = {"M": M, "K": k, "N": n, "ms": ms, "tflops": fl / ms / 1e9,
+                     "frac_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS}
+        wb.free()
+    qkv = gpu.new(M * 3 * H, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, qkv.h, 0, M * 3 * H, 1, 3, 1.0, 0.0), "fill")
+    att = gpu.new(M * H, qd.BF16)
+    R = TEXT + GH * GW
+    run = lambda: gpu.attention(att, qkv, qkv, qkv, BATCH, R, R, CFG["heads"], 3 * H, 3 * H,  # noqa
+                                3 * H, H, 0, H, 2 * H, text_rows=TEXT, text_causal=0)
+    run()
+    ms = time_ms(gpu, run, reps)
+    _, sd, _ = flops(dict(CFG, layers=1), R, TEXT, BATCH)
+    res["attention"] = {"batch": BATCH, "q_rows": R, "heads": CFG["heads"], "ms": ms,
+                        "tflops": sd / ms / 1e9, "frac_peak": sd / ms / 1e9 / PEAK_BF16_TFLOPS}
+    return res
+
+
+def cpu_baseline(blocks=3):
+    """`blocks` of the 32 blocks, one CFG branch, full rows, on the host
+    oracle; scaled to a step (32 blocks x 2 branches)."""
+    from oracle import oracle as o
+    R, H = TEXT + GH * GW, CFG["hidden"]
+    t0 = time.time()
+    m = o.Model(dict(CFG, layers=blocks), SEED, blocks)
+    hid = o.fill_normal_bf16(R * H, SEED, 990)
+    mod = o.fill_normal_bf16(2 * 6 * H, SEED, 991, 0.2)
+    rm = (np.arange(R) < TEXT).astype(np.uint32)
+    cos, sin = o.rope_tables(TEXT, GH, GW)
+    setup = time.time() - t0
+    t1 = time.time()
+    for layer in range(blocks):
+        m.block(layer, hid, mod, cos, sin, rm, R, TEXT)
+    block_s = (time.time() - t1) / blocks
+    m.close()
+    per_step_ms = block_s * 1e3 * CFG["layers"] * BATCH
+    return {"value": per_step_ms, "unit": "ms/step", "cores": o.lib().qo_num_threads(),
+            "kind": "port",
+            "sample": f"{blocks} of {CFG['layers']} blocks x 1 of {BATCH} CFG branches at the "
+                      f"full {R}-row shape (int8 weights): {block_s:.2f} s per block measured, "
+                      f"scaled x{CFG['layers'] * BATCH}; weight generation {setup:.1f} s "
+                      f"excluded"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-breakdown", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    qd = load_qdit()
+    gpu = qd.Gpu()
+    R, I = TEXT + GH * GW, GH * GW
+    L = qd.lib()
+    t0 = time.time()
+    dit = qd.Dit(gpu, CFG, SEED)
+    text = gpu.new(BATCH * TEXT * CFG["text_dim"], qd.BF16)
+    lat = gpu.new(BATCH * I * CFG["z_dim"], qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, text.h, 0, text.n, SEED, 800, 1.0, 0.0), "fill")
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, lat.h, 0, lat.n, SEED, 801, 1.0, 0.0), "fill")
+    cos = np.empty((R, 64), np.float32)
+    sin = np.empty((R, 64), np.float32)
+    L.qw_pipe_rope_tables_host(TEXT, GH, GW, cos.ctypes.data, sin.ctypes.data)
+    cos_t, sin_t = gpu.put(cos), gpu.put(sin)
+    out = gpu.new(BATCH * R * CFG["z_dim"], qd.BF16)
+    gpu.submit()
+    setup_s = time.time() - t0
+
+    step = lambda: dit.forward_batch(text, TEXT, lat, I, BATCH, SIGMA, cos_t, sin_t, out)  # noqa
+    for _ in range(args.warmup):
+        step()
+    gpu.submit()
+    gpu.timer_begin()
+    w0 = time.time()
+    for _ in range(args.steps):
+        step()
+    dev_ms = gpu.timer_end()
+    gpu.submit()
+    wall_ms = (time.time() - w0) * 1e3
+    ms_step = dev_ms / args.steps
+    v = out.read().view(np.uint16)
+    finite = bool(np.all((v & 0x7F80) != 0x7F80))
+
+    lin, sdpa, extra = flops(CFG, R, TEXT, BATCH)
+    total_tflops = (lin + sdpa + extra) / ms_step / 1e9
+    brk = {} if args.no_breakdown else kernel_breakdown(qd, gpu)
+    up = brk.get("up")
+    roofline = None
+    if up:
+        fl = 2.0 * up["M"] * up["N"] * up["K"]
+        achieved = fl / up["ms"] / 1e9
+        roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                    "kernel": "qw_gemm_i8_gelu (up-projection, M=8704 K=3072 N=12288)",
+                    "ms_per_launch": up["ms"]}
+    cpu = None if args.no_cpu else cpu_baseline()
+    line = {
+        "metric": "DiT ms/step @1024^2 (4352 tok, CFG b=2); linear+SDPA TFLOP/s & % MFMA peak",
+        "value": ms_step, "unit": "ms/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 (int8 weight-only linears)",
+        "data": "synthetic (seeded device generator; random-init weights)",
+        "config": {"workload": "BASELINE configs[4]: 32-layer DiT, 1024^2, 4096 image + 256 "
+                               "text tokens, CFG batch 2, int8 weight-only linears",
+                   "hidden": CFG["hidden"], "heads": CFG["heads"], "mlp": CFG["mlp_width"],
+                   "rows_per_linear": BATCH * R, "layers": CFG["layers"]},
+        "step_tflops": total_tflops,
+        "step_frac_peak": total_tflops / PEAK_BF16_TFLOPS,
+        "flop_per_step": {"linear": lin, "sdpa": sdpa, "other": extra},
+        "breakdown": brk,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "wall_ms_per_step": wall_ms / args.steps,
+        "setup_s": setup_s,
+        "output_finite": finite,
+    }
+    print(json.dumps(line))
+    dit.close()
+    gpu.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -183,8 +183,13 @@ def test_layer_norm_mod(gpu, qd, oracle, width, shift):
     gpu.submit()
     ref = np.empty(rows * width, np.uint16)
     oracle.lib().qo_layer_norm_mod(ref, x, mod, rm, rows, width, slots, 1, 5 if shift else -1, 1e-6)
-    d = ulp_diff(out.read(), ref)
-    assert d.max() <= 1 and np.mean(d == 0) > 0.99
+    got = out.read()
+    d = ulp_diff(got, ref)
+    # outputs are O(1); with a shift, x_hat (1 + s) + shift can cancel to
+    # near zero, where one fp32 ulp of the O(1) terms is many bf16 ulps of
+    # the result: bound those by an absolute 2^-9 instead
+    diff = np.abs(oracle.bf16_to_f32(got) - oracle.bf16_to_f32(ref))
+    assert np.all((d <= 1) | (diff <= 2.0 ** -9)) and np.mean(d == 0) > 0.99
 
 
 @pytest.mark.parametrize("case,text,rows", [("a", 0, 16), ("b", 8, 20)])
