@@ -23,7 +23,9 @@ enum {
     K_LN_MOD, K_RMS_ONE, K_QK_NORM_ROPE, K_GATE, K_ACT, K_SWIGLU, K_CAST,
     K_REORDER, K_FILL, K_QUANT, K_DEQUANT, K_COPY2D, K_ATTN,
     K_GEMM_BF16_STORE, K_GEMM_BF16_GELU, K_GEMM_BF16_GATE,
-    K_GEMM_I8_STORE, K_GEMM_I8_GELU, K_GEMM_I8_GATE, K_COUNT
+    K_GEMM_I8_STORE, K_GEMM_I8_GELU, K_GEMM_I8_GATE,
+    K_GEMM_BF16_STORE_W8, K_GEMM_BF16_GELU_W8, K_GEMM_BF16_GATE_W8,
+    K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_bf16", "qw_rms_norm_one_bf16", "qw_qk_norm_rope_bf16",
@@ -31,7 +33,9 @@ static const char *k_names[K_COUNT] = {
     "qw_modulation_reorder_bf16", "qw_fill_normal_bf16", "qw_quantize_int8_rows",
     "qw_dequant_int8_f32", "qw_copy2d", "qw_attention_bf16",
     "qw_gemm_bf16_store", "qw_gemm_bf16_gelu", "qw_gemm_bf16_gate",
-    "qw_gemm_i8_store", "qw_gemm_i8_gelu", "qw_gemm_i8_gate"};
+    "qw_gemm_i8_store", "qw_gemm_i8_gelu", "qw_gemm_i8_gate",
+    "qw_gemm_bf16_store_w8", "qw_gemm_bf16_gelu_w8", "qw_gemm_bf16_gate_w8",
+    "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8"};
 
 struct h3_gpu {
     int device;
@@ -693,6 +697,9 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
         return fail(g, "linear: input rows must be 16-byte aligned (lda %u, offset %zu)", d->lda,
                     d->in_offset);
     if (d->ldc < d->cols) return fail(g, "linear: ldc < cols");
+    if (d->cols % 8 || d->ldc % 4 || d->out_offset % 4)
+        return fail(g, "linear: cols (%u) must be a multiple of 8 and output rows 8-byte aligned",
+                    d->cols);
     if (!fits(d->in, d->in_offset, (size_t)(d->rows - 1) * d->lda + d->k))
         return fail(g, "linear: input too small");
     if (!fits(d->out, d->out_offset, (size_t)(d->rows - 1) * d->ldc + d->cols))
@@ -737,10 +744,26 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     a.lda = d->lda;
     a.ldc = d->ldc;
     a.gate_row_stride = gate_stride;
+    {
+        const uint64_t ab = ((uint64_t)(d->rows - 1) * d->lda + d->k) * 2;
+        const uint64_t wb = (uint64_t)d->cols * d->k * (int8 ? 1 : 2);
+        if (ab >= (1ull << 31) || wb >= (1ull << 31))
+            return fail(g, "linear: operand exceeds 2 GiB buffer range");
+        a.a_bytes = (uint32_t)ab;
+        a.w_bytes = (uint32_t)wb;
+    }
     a.tiles_m = (d->rows + 255) / 256;
     a.tiles_n = (d->cols + 255) / 256;
+    /* both GEMM shapes cover 256 x 256 per workgroup; QW_GEMM_SHAPE=b
+     * selects the 8-wave variant (two waves per SIMD) */
+    static int shape_b = -1;
+    if (shape_b < 0) {
+        const char *e = getenv("QW_GEMM_SHAPE");
+        shape_b = e && e[0] == 'b';
+    }
     int kid = (int8 ? K_GEMM_I8_STORE : K_GEMM_BF16_STORE) + d->epilogue;
-    return launch(g, kid, dim3(a.tiles_m * a.tiles_n), dim3(256), a);
+    if (shape_b) kid += K_GEMM_BF16_STORE_W8 - K_GEMM_BF16_STORE;
+    return launch(g, kid, dim3(a.tiles_m * a.tiles_n), dim3(shape_b ? 512 : 256), a);
 }
 
 static qw_linear_desc plain_linear(h3_gpu_tensor *out, const h3_gpu_tensor *in,

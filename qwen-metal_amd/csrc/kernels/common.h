@@ -64,12 +64,15 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
 }
 
 /* h3_shaders.metal:3385-3408 (approximate = 1): GELU with the tanh form,
- * saturating outside |inner| < 10. */
+ * saturating outside |inner| < 10. Evaluated through the identity
+ * 0.5 (1 + tanh u) = 1 / (1 + e^(-2u)): one v_exp_f32 and one v_rcp_f32,
+ * no cancellation for negative u (the 1 + tanh form loses bits there). */
 __device__ __forceinline__ float gelu_tanh_f(float v) {
     float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
     if (inner <= -10.0f) return 0.0f;
     if (inner >= 10.0f) return v;
-    return 0.5f * v * (1.0f + tanhf(inner));
+    const float e = __builtin_amdgcn_exp2f(inner * -2.8853900817779268f); /* e^(-2u) */
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }

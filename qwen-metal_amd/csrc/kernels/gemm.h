@@ -4,27 +4,45 @@
  * layout (bf16, or int8 with one fp32 scale per output row), fp32
  * accumulation in v_mfma_f32_32x32x16_bf16.
  *
- * Tiling: 256 x 256 x 64 macro-tile per workgroup of 4 waves (2 x 2, each
- * wave 128 x 128 = 4 x 4 MFMA blocks of 32 x 32, 256 fp32 accumulators per
- * lane). A and W tiles are staged through LDS, double-buffered (2 x 64 KB),
- * with the next K-slice's global loads in flight while the current one is
- * multiplied. LDS rows are 128 B; 16-byte chunks are XOR-swizzled by
- * (row / 2) % 8 so the 32 rows one MFMA operand read touches spread over
- * all banks. int8 weights are widened to bf16 (exact for |q| <= 127) on the
- * way into LDS, and the per-row scale multiplies the fp32 sum in the
- * epilogue, so the contraction equals the dequantised product.
+ * Tiling (template): a workgroup of WM x WN waves computes a BM x BN tile,
+ * BM = WM * MI * 32, BN = WN * NI * 32, each wave an (MI*32) x (NI*32) block
+ * of MI x NI MFMA tiles, stepping K by 64. Shapes in use:
+ *   A: 2 x 2 waves of 4 x 4 blocks (256 x 256, one wave per SIMD, 256
+ *      accumulators per lane);
+ *   B: 4 x 2 waves of 2 x 4 blocks (256 x 256, two waves per SIMD, 128
+ *      accumulators each: one wave's MFMAs cover the other's LDS/global
+ *      latency).
+ * A and W tiles are staged through LDS, double-buffered (2 x 64 KB at
+ * 256 x 256), with the next K-slice's global loads in flight while the
+ * current one is multiplied; within a K-slice the operand fragments of
+ * sub-step s + 1 are read from LDS while the MFMAs of sub-step s run. LDS
+ * rows are 128 B; 16-byte chunks are XOR-swizzled by (row / 2) % 8: the
+ * 64 banks (256 B) serve 16 lanes of a ds_read_b128 per pass, and 16
+ * consecutive rows then land on 16 distinct (bank half, chunk) slots (an
+ * earlier row % 8 swizzle measured 2.3x more bank-conflict cycles). int8
+ * weights are widened to bf16 (exact for |q| <= 127) on the way into LDS and the
+ * per-row scale multiplies the fp32 sum in the epilogue, so the contraction
+ * equals the dequantised product.
+ *
+ * The MFMA is issued as C^T = W A^T (W fragment as the A operand): each
+ * lane then holds, for one output row, runs of 4 consecutive output
+ * columns, stored as 8-byte writes with the epilogue (scale, bias, GELU,
+ * residual gate) applied in registers.
  *
  * Tile order: workgroup ids are dealt round-robin to the 8 XCDs; the id is
  * remapped so each XCD owns a contiguous range of tiles, walked in groups
- * of 8 tile-rows, keeping the A panels and W panels an XCD touches hot in
- * its own L2. */
+ * of 8 tile-rows, keeping the A and W panels an XCD touches hot in its L2. */
 #pragma once
 #include "common.h"
 
-#define GBM 256
-#define GBN 256
 #define GBK 64
-#define G_LDS_BUF 65536 /* A (32 KB) + W (32 KB) per stage */
+/* QW_EXP_FIXED_K (experiments only, never in the shipped build): every
+ * K-slice load re-reads slice 0, isolating global-memory effects. */
+#ifdef QW_EXP_FIXED_K
+#define QW_K(x) 0
+#else
+#define QW_K(x) (x)
+#endif
 
 __device__ __forceinline__ uint32_t g_swz(uint32_t row, uint32_t chunk) {
     return row * 128u + ((chunk ^ ((row >> 1) & 7u)) << 4);
@@ -47,10 +65,127 @@ __device__ __forceinline__ void i8x16_to_bf16(u32x4 q, u32x4 &lo, u32x4 &hi) {
     hi = u32x4{o[4], o[5], o[6], o[7]};
 }
 
-template <int EPI, int INT8>
-__device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned char *lds) {
+template <int WM, int WN, int MI, int NI>
+struct GemmShape {
+    static constexpr int NT = 64 * WM * WN;
+    static constexpr int BM = WM * MI * 32;
+    static constexpr int BN = WN * NI * 32;
+    static constexpr int A_BYTES = BM * 128; /* BM rows x 64 bf16 */
+    static constexpr int W_BYTES = BN * 128;
+    static constexpr int STAGE = A_BYTES + W_BYTES;
+    static constexpr int A_LD = BM * 8 / NT;        /* 16-byte A chunks per thread */
+    static constexpr int W_LD_BF16 = BN * 8 / NT;   /* 16-byte bf16 W chunks */
+    static constexpr int W_LD_I8 = BN * 4 / NT;     /* 16-byte int8 W chunks */
+};
+
+/* Operands of one pipelined K-slice (direct-to-LDS path). */
+template <int A_DL, int W_DL, int WLD>
+struct PipeCtx {
+    __amdgpu_buffer_rsrc_t a_rsrc, w_rsrc;
+    uint32_t a_dvoff[A_DL];
+    uint32_t w_dvoff[W_DL > 0 ? W_DL : 1];
+    uint32_t w_off[WLD];
+    uint32_t a_row0, w_row0, swz, h, a_dst0, w_dst0, wr, wc;
+};
+
+/* One K-slice: multiply the stage `cur` while slice k_next streams into the
+ * stage `nxt`. The two stages are distinct (restrict) so the scheduler may
+ * interleave the LDS fragment reads of one with the direct loads into the
+ * other; sched_group_barrier then lays out the pipeline: fragment reads of
+ * sub-step s + 1, the slice loads and the int8 LDS writes between MFMAs. */
+template <int INT8, int MI, int NI, int A_BYTES, int A_DL, int W_DL, int WLD, int WROWS>
+__device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &c,
+                                                floatx16 (&acc)[NI][MI],
+                                                const unsigned char *__restrict__ cur,
+                                                unsigned char *__restrict__ nxt,
+                                                uint32_t k_next) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    /* slice k_next: A (and bf16 W) straight into LDS */
+#pragma unroll
+    for (int j = 0; j < A_DL; j++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.a_rsrc, (lds_void *)(nxt + c.a_dst0 + j * 1024),
+                                                 16, c.a_dvoff[j] + k_next * 2, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < W_DL; j++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.w_rsrc,
+                                                 (lds_void *)(nxt + A_BYTES + c.w_dst0 + j * 1024),
+                                                 16, c.w_dvoff[j] + k_next * 2, 0, 0, 0);
+    u32x4 rw[WLD];
+    if (INT8) {
+#pragma unroll
+        for (int j = 0; j < WLD; j++)
+            rw[j] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(c.w_rsrc, c.w_off[j] + k_next, 0, 0));
+    }
+    /* MFMAs of this slice, fragments double-buffered across sub-steps */
+    const unsigned char *As = cur, *Ws = cur + A_BYTES;
+#define QW_FR(row, ks) ((row) * 128u + (((2 * (ks) + c.h) ^ c.swz) << 4))
+    bf16x8 af[2][MI], bw[2][NI];
+#pragma unroll
+    for (int i = 0; i < MI; i++) af[0][i] = *(const bf16x8 *)(As + QW_FR(c.a_row0 + 32 * i, 0));
+#pragma unroll
+    for (int i = 0; i < NI; i++) bw[0][i] = *(const bf16x8 *)(Ws + QW_FR(c.w_row0 + 32 * i, 0));
+#pragma unroll
+    for (uint32_t ks = 0; ks < 4; ks++) {
+        const int b = ks & 1;
+        if (ks + 1 < 4) {
+#pragma unroll
+            for (int i = 0; i < MI; i++)
+                af[b ^ 1][i] = *(const bf16x8 *)(As + QW_FR(c.a_row0 + 32 * i, ks + 1));
+#pragma unroll
+            for (int i = 0; i < NI; i++)
+                bw[b ^ 1][i] = *(const bf16x8 *)(Ws + QW_FR(c.w_row0 + 32 * i, ks + 1));
+        }
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int mi = 0; mi < MI; mi++)
+                acc[ni][mi] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[b][ni], af[b][mi],
+                                                                      acc[ni][mi], 0, 0, 0);
+    }
+#undef QW_FR
+    if (INT8) {
+        unsigned char *Wn = nxt + A_BYTES;
+#pragma unroll
+        for (int j = 0; j < WLD; j++) {
+            u32x4 lo, hi;
+            i8x16_to_bf16(rw[j], lo, hi);
+            const uint32_t r = c.wr + WROWS * j;
+            *(u32x4 *)(Wn + g_swz(r, 2 * c.wc)) = lo;
+            *(u32x4 *)(Wn + g_swz(r, 2 * c.wc + 1)) = hi;
+        }
+    }
+    constexpr int NMF = MI * NI, NRD = MI + NI;
+    constexpr int NV = A_DL + W_DL + (INT8 ? WLD : 0);
+    constexpr int NW = INT8 ? 2 * WLD : 0;
+    static_assert(NV <= NMF && NW <= NMF && NRD <= NMF, "pipeline pattern");
+    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0); /* fragments of step 0 */
+#pragma unroll
+    for (int i = 0; i < NMF; i++) { /* step 0: slice loads + fragments of step 1 */
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i < NV) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+#pragma unroll
+    for (int st = 1; st < 3; st++)
+#pragma unroll
+        for (int i = 0; i < NMF; i++) { /* steps 1, 2: fragments of the next step */
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+#pragma unroll
+    for (int i = 0; i < NMF; i++) { /* step 3: int8 W writes of slice k_next */
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i < NW) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    }
+}
+
+template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int FDB>
+__device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned char *lds,
+                                             unsigned char *lds_b) {
+    typedef GemmShape<WM, WN, MI, NI> S;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t wm = wave >> 1, wn = wave & 1;
+    const uint32_t wm = wave / WN, wn = wave % WN;
     const uint32_t h = lane >> 5, i32 = lane & 31;
 
     /* ---- tile id -> (tm, tn), XCD-contiguous, grouped by 8 tile-rows ---- */
@@ -63,141 +198,289 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     const uint32_t gsize = min(a.tiles_m - first_m, G);
     const uint32_t inner = pid % per_group;
     const uint32_t tm = first_m + inner % gsize, tn = inner / gsize;
-    const uint32_t m0 = tm * GBM, n0 = tn * GBN;
+    const uint32_t m0 = tm * S::BM, n0 = tn * S::BN;
 
-    /* ---- global load coordinates (row-clamped at the edges) ------------- */
-    const u16 *A = (const u16 *)a.a;
-    const uint32_t ac = tid & 7, ar = tid >> 3; /* A: 8 chunks x 32 rows per pass */
-    uint32_t a_off[8];
+    /* ---- global loads: raw buffer loads with 32-bit byte offsets (one
+     *      VGPR per load address), rows clamped at the edges ------------- */
+    const __amdgpu_buffer_rsrc_t a_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.a, (short)0, (int)a.a_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.w, (short)0, (int)a.w_bytes, 0x00020000);
+    const uint32_t ac = tid & 7, ar = tid >> 3; /* 8 chunks per 64-wide row */
+    constexpr int AROWS = S::NT / 8;             /* rows per load pass */
+    uint32_t a_off[S::A_LD];
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        uint32_t r = min(m0 + ar + 32 * j, a.m - 1);
-        a_off[j] = r * a.lda + ac * 8;
+    for (int j = 0; j < S::A_LD; j++) {
+        uint32_t r = min(m0 + ar + AROWS * j, a.m - 1);
+        a_off[j] = (r * a.lda + ac * 8) * 2;
     }
-    constexpr int WLD = INT8 ? 4 : 8;
+    constexpr int WLD = INT8 ? S::W_LD_I8 : S::W_LD_BF16;
+    constexpr int WROWS = INT8 ? S::NT / 4 : S::NT / 8;
+    constexpr uint32_t WES = INT8 ? 1 : 2; /* weight element bytes */
     const uint32_t wc = INT8 ? (tid & 3) : (tid & 7);
     const uint32_t wr = INT8 ? (tid >> 2) : (tid >> 3);
     uint32_t w_off[WLD];
 #pragma unroll
     for (int j = 0; j < WLD; j++) {
-        uint32_t r = min(n0 + wr + (INT8 ? 64 : 32) * j, a.n - 1);
-        w_off[j] = r * a.k + wc * (INT8 ? 16 : 8);
+        uint32_t r = min(n0 + wr + WROWS * j, a.n - 1);
+        w_off[j] = (r * a.k + wc * (INT8 ? 16 : 8)) * WES;
     }
 
-    u32x4 ra[8], rw[WLD];
-    auto load_global = [&](uint32_t k0) {
+    /* PF staging register sets: slice kt + PF is loaded while slice kt is
+     * multiplied (set index = slice % PF), then slice kt + 1 is written to
+     * the other LDS buffer; PF = 2 gives loads two slices to land */
+    u32x4 ra[PF > 0 ? PF : 1][S::A_LD], rw[PF > 0 ? PF : 1][WLD];
+#define QW_LOAD(SET, k0)                                                                      \
+    do {                                                                                       \
+        _Pragma("unroll") for (int j = 0; j < S::A_LD; j++) ra[SET][j] = __builtin_bit_cast(   \
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(a_rsrc, a_off[j] + (k0) * 2, 0, 0));  \
+        _Pragma("unroll") for (int j = 0; j < WLD; j++) rw[SET][j] = __builtin_bit_cast(       \
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, w_off[j] + (k0) * WES, 0, 0)); \
+    } while (0)
+    auto store_lds = [&](const u32x4 *sa, const u32x4 *sw, uint32_t buf)
+                         __attribute__((always_inline)) {
+        unsigned char *As = lds + buf * S::STAGE;
+        unsigned char *Ws = As + S::A_BYTES;
 #pragma unroll
-        for (int j = 0; j < 8; j++) ra[j] = *(const u32x4 *)(A + a_off[j] + k0);
-        if (INT8) {
-            const int8_t *W = (const int8_t *)a.w;
-#pragma unroll
-            for (int j = 0; j < WLD; j++) rw[j] = *(const u32x4 *)(W + w_off[j] + k0);
-        } else {
-            const u16 *W = (const u16 *)a.w;
-#pragma unroll
-            for (int j = 0; j < WLD; j++) rw[j] = *(const u32x4 *)(W + w_off[j] + k0);
-        }
-    };
-    auto store_lds = [&](uint32_t buf) {
-        unsigned char *As = lds + buf * G_LDS_BUF;
-        unsigned char *Ws = As + 32768;
-#pragma unroll
-        for (int j = 0; j < 8; j++) *(u32x4 *)(As + g_swz(ar + 32 * j, ac)) = ra[j];
+        for (int j = 0; j < S::A_LD; j++) *(u32x4 *)(As + g_swz(ar + AROWS * j, ac)) = sa[j];
         if (INT8) {
 #pragma unroll
             for (int j = 0; j < WLD; j++) {
                 u32x4 lo, hi;
-                i8x16_to_bf16(rw[j], lo, hi);
-                const uint32_t r = wr + 64 * j;
+                i8x16_to_bf16(sw[j], lo, hi);
+                const uint32_t r = wr + WROWS * j;
                 *(u32x4 *)(Ws + g_swz(r, 2 * wc)) = lo;
                 *(u32x4 *)(Ws + g_swz(r, 2 * wc + 1)) = hi;
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < WLD; j++) *(u32x4 *)(Ws + g_swz(wr + 32 * j, wc)) = rw[j];
+            for (int j = 0; j < WLD; j++) *(u32x4 *)(Ws + g_swz(wr + WROWS * j, wc)) = sw[j];
         }
     };
 
-    floatx16 acc[4][4];
+    floatx16 acc[NI][MI]; /* C^T blocks */
 #pragma unroll
-    for (int mi = 0; mi < 4; mi++)
+    for (int ni = 0; ni < NI; ni++)
 #pragma unroll
-        for (int ni = 0; ni < 4; ni++)
+        for (int mi = 0; mi < MI; mi++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) acc[mi][ni][v] = 0.0f;
+            for (int v = 0; v < 16; v++) acc[ni][mi][v] = 0.0f;
+
+    /* fragment rows: this lane's row within each 32-row block; the swizzle
+     * term (row / 2) % 8 only depends on i32 (blocks are 32-aligned) */
+    const uint32_t a_row0 = wm * (MI * 32) + i32, w_row0 = wn * (NI * 32) + i32;
+    const uint32_t swz = (i32 >> 1) & 7u;
+#define QW_FRAG(row, ks) ((row) * 128u + (((2 * (ks) + h) ^ swz) << 4))
 
     const uint32_t KT = a.k / GBK;
-    load_global(0);
-    store_lds(0);
-    __syncthreads();
-    for (uint32_t kt = 0; kt < KT; kt++) {
-        const uint32_t cur = kt & 1;
-        if (kt + 1 < KT) load_global((kt + 1) * GBK);
-        const unsigned char *As = lds + cur * G_LDS_BUF;
-        const unsigned char *Ws = As + 32768;
+#define QW_COMPUTE_AT(base)                                                                     \
+    do {                                                                                        \
+        const unsigned char *As = (base);                                                       \
+        const unsigned char *Ws = As + S::A_BYTES;                                              \
+        bf16x8 af[1 + FDB][MI], bw[1 + FDB][NI];                                                \
+        _Pragma("unroll") for (int i = 0; i < MI; i++) af[0][i] =                               \
+            *(const bf16x8 *)(As + QW_FRAG(a_row0 + 32 * i, 0));                                \
+        _Pragma("unroll") for (int i = 0; i < NI; i++) bw[0][i] =                               \
+            *(const bf16x8 *)(Ws + QW_FRAG(w_row0 + 32 * i, 0));                                \
+        _Pragma("unroll") for (uint32_t ks = 0; ks < 4; ks++) {                                 \
+            const int c = FDB ? (ks & 1) : 0;                                                   \
+            if (!FDB && ks > 0) {                                                               \
+                _Pragma("unroll") for (int i = 0; i < MI; i++) af[0][i] =                       \
+                    *(const bf16x8 *)(As + QW_FRAG(a_row0 + 32 * i, ks));                       \
+                _Pragma("unroll") for (int i = 0; i < NI; i++) bw[0][i] =                       \
+                    *(const bf16x8 *)(Ws + QW_FRAG(w_row0 + 32 * i, ks));                       \
+            }                                                                                   \
+            if (FDB && ks + 1 < 4) {                                                            \
+                _Pragma("unroll") for (int i = 0; i < MI; i++) af[c ^ FDB][i] =                 \
+                    *(const bf16x8 *)(As + QW_FRAG(a_row0 + 32 * i, ks + 1));                   \
+                _Pragma("unroll") for (int i = 0; i < NI; i++) bw[c ^ FDB][i] =                 \
+                    *(const bf16x8 *)(Ws + QW_FRAG(w_row0 + 32 * i, ks + 1));                   \
+            }                                                                                   \
+            _Pragma("unroll") for (int ni = 0; ni < NI; ni++)                                   \
+                _Pragma("unroll") for (int mi = 0; mi < MI; mi++) acc[ni][mi] =                 \
+                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[c][ni], af[c][mi], acc[ni][mi],  \
+                                                            0, 0, 0);                           \
+        }                                                                                       \
+    } while (0)
+#define QW_COMPUTE(cur) QW_COMPUTE_AT(lds + (cur) * S::STAGE)
+    if (PF == 0) {
+        /* Direct-to-LDS pipeline. The A tile (and a bf16 W tile) are loaded
+         * with buffer_load_dwordx4 ... lds: each instruction writes 1 KB
+         * (8 rows) of a wave's share of the tile straight into LDS, lane l
+         * landing on row l / 8, physical chunk l % 8; the lane therefore
+         * fetches logical chunk (l % 8) ^ ((row / 2) % 8), which realises
+         * the swizzle with no staging registers and no ds_write. int8 W is
+         * still widened through registers. The last slice re-loads itself
+         * into the idle stage, which nobody reads afterwards. */
+        constexpr int NWAVE = WM * WN;
+        constexpr int A_DL = S::BM / 8 / NWAVE;  /* direct loads per wave, A */
+        constexpr int W_DL = INT8 ? 0 : S::BN / 8 / NWAVE;
+        PipeCtx<A_DL, W_DL, WLD> c;
+        c.a_rsrc = a_rsrc;
+        c.w_rsrc = w_rsrc;
+        const uint32_t lrow = lane >> 3, lp = lane & 7;
 #pragma unroll
-        for (uint32_t ks = 0; ks < 4; ks++) {
-            bf16x8 af[4], bw[4];
-#pragma unroll
-            for (int mi = 0; mi < 4; mi++)
-                af[mi] = *(const bf16x8 *)(As + g_swz(wm * 128 + mi * 32 + i32, 2 * ks + h));
-#pragma unroll
-            for (int ni = 0; ni < 4; ni++)
-                bw[ni] = *(const bf16x8 *)(Ws + g_swz(wn * 128 + ni * 32 + i32, 2 * ks + h));
-#pragma unroll
-            for (int mi = 0; mi < 4; mi++)
-#pragma unroll
-                for (int ni = 0; ni < 4; ni++)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bw[ni],
-                                                                          acc[mi][ni], 0, 0, 0);
+        for (int j = 0; j < A_DL; j++) {
+            const uint32_t r = wave * (S::BM / NWAVE) + j * 8 + lrow;
+            c.a_dvoff[j] = (min(m0 + r, a.m - 1) * a.lda + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
         }
-        if (kt + 1 < KT) store_lds(cur ^ 1);
+#pragma unroll
+        for (int j = 0; j < W_DL; j++) {
+            const uint32_t r = wave * (S::BN / NWAVE) + j * 8 + lrow;
+            c.w_dvoff[j] = (min(n0 + r, a.n - 1) * a.k + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+        }
+#pragma unroll
+        for (int j = 0; j < WLD; j++) c.w_off[j] = w_off[j];
+        c.a_row0 = a_row0;
+        c.w_row0 = w_row0;
+        c.swz = swz;
+        c.h = h;
+        c.a_dst0 = wave * (S::BM / NWAVE) * 128;
+        c.w_dst0 = wave * (S::BN / NWAVE) * 128;
+        c.wr = wr;
+        c.wc = wc;
+        /* prologue: slice 0 into stage lds (A/W direct; int8 W via regs) */
+        {
+            typedef __attribute__((address_space(3))) void lds_void;
+#pragma unroll
+            for (int j = 0; j < A_DL; j++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(lds + c.a_dst0 + j * 1024),
+                                                         16, c.a_dvoff[j], 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < W_DL; j++)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    w_rsrc, (lds_void *)(lds + S::A_BYTES + c.w_dst0 + j * 1024), 16, c.w_dvoff[j], 0,
+                    0, 0);
+            if (INT8) {
+                QW_LOAD(0, 0);
+                store_lds(ra[0], rw[0], 0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): direct loads landed */
         __syncthreads();
+        for (uint32_t kt = 0; kt < KT; kt++) {
+            const uint32_t odd = kt & 1;
+            const uint32_t nk = (kt + 1 < KT ? kt + 1 : kt) * GBK;
+            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS>(
+                c, acc, odd ? lds_b : lds, odd ? lds : lds_b, QW_K(nk));
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+        }
+    } else if (PF == 1) {
+        QW_LOAD(0, 0);
+        store_lds(ra[0], rw[0], 0);
+        __syncthreads();
+        for (uint32_t kt = 0; kt < KT; kt++) {
+            const uint32_t cur = kt & 1;
+            if (kt + 1 < KT) QW_LOAD(0, QW_K((kt + 1) * GBK));
+            QW_COMPUTE(cur);
+            if (kt + 1 < KT) store_lds(ra[0], rw[0], cur ^ 1);
+            __syncthreads();
+        }
+    } else {
+        /* slice j: register set j % 2, LDS buffer j % 2 */
+        QW_LOAD(0, 0);
+        if (KT > 1) QW_LOAD(PF - 1, QW_K(GBK));
+        store_lds(ra[0], rw[0], 0);
+        __syncthreads();
+        for (uint32_t kt = 0; kt < KT; kt += 2) {
+            if (kt + 2 < KT) QW_LOAD(0, QW_K((kt + 2) * GBK));
+            QW_COMPUTE(0);
+            if (kt + 1 < KT) store_lds(ra[PF - 1], rw[PF - 1], 1);
+            __syncthreads();
+            if (kt + 1 >= KT) break;
+            if (kt + 3 < KT) QW_LOAD(PF - 1, QW_K((kt + 3) * GBK));
+            QW_COMPUTE(1);
+            if (kt + 2 < KT) store_lds(ra[0], rw[0], 0);
+            __syncthreads();
+        }
     }
+#undef QW_COMPUTE
+#undef QW_COMPUTE_AT
+#undef QW_LOAD
+#undef QW_FRAG
 
-    /* ---- epilogue: lane holds column i32 of each 32x32 block, rows
-     *      8 * (v / 4) + 4 * h + v % 4 -------------------------------------- */
+    /* ---- epilogue: acc[ni][mi][4g + j] = C[row, col] with
+     *      row = m0 + wm*MI*32 + mi*32 + i32,
+     *      col = n0 + wn*NI*32 + ni*32 + 8g + 4h + j ----------------------- */
     {
 #pragma clang fp contract(off)
 #pragma unroll
-    for (int ni = 0; ni < 4; ni++) {
-        const uint32_t col = n0 + wn * 128 + ni * 32 + i32;
-        if (col >= a.n) continue;
-        const float sc = INT8 ? a.wscale[col] : 1.0f;
-        const float bias = a.bias ? bf2f(a.bias[col]) : 0.0f;
+        for (int ni = 0; ni < NI; ni++) {
 #pragma unroll
-        for (int mi = 0; mi < 4; mi++) {
+            for (int g = 0; g < 4; g++) {
+                const uint32_t col = n0 + wn * (NI * 32) + ni * 32 + 8 * g + 4 * h;
+                if (col >= a.n) continue; /* n % 8 == 0: a group is all in or out */
+                floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
+                if (INT8) sc = *(const floatx4 *)(a.wscale + col);
+                float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (a.bias) {
+                    const u32x2 bb = *(const u32x2 *)(a.bias + col);
+                    bias[0] = lo_bf(bb[0]);
+                    bias[1] = hi_bf(bb[0]);
+                    bias[2] = lo_bf(bb[1]);
+                    bias[3] = hi_bf(bb[1]);
+                }
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                if (row >= a.m) continue;
-                float y = acc[mi][ni][v];
-                if (INT8) y *= sc;
-                y += bias;
-                u16 *dst = a.out + (size_t)row * a.ldc + col;
-                if (EPI == QW_EPI_STORE) {
-                    *dst = f2bf(y);
-                } else if (EPI == QW_EPI_GELU) {
-                    *dst = f2bf(gelu_tanh_f(bf2f(f2bf(y))));
-                } else {
-                    const float g = bf2f(a.gate[(size_t)a.row_map[row] * a.gate_row_stride + col]);
-                    *dst = f2bf(bf2f(*dst) + bf2f(f2bf(y)) * g);
+                for (int mi = 0; mi < MI; mi++) {
+                    const uint32_t row = m0 + wm * (MI * 32) + mi * 32 + i32;
+                    if (row >= a.m) continue;
+                    float y[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        float t = acc[ni][mi][4 * g + j];
+                        if (INT8) t *= sc[j];
+                        y[j] = bf2f(f2bf(t + bias[j]));
+                    }
+                    u16 *dst = a.out + (size_t)row * a.ldc + col;
+                    if (EPI == QW_EPI_GELU) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) y[j] = gelu_tanh_f(y[j]);
+                    } else if (EPI == QW_EPI_GATE) {
+                        const u32x2 gv = *(const u32x2 *)(a.gate +
+                                                          (size_t)a.row_map[row] * a.gate_row_stride + col);
+                        const u32x2 rv = *(const u32x2 *)dst;
+                        y[0] = lo_bf(rv[0]) + y[0] * lo_bf(gv[0]);
+                        y[1] = hi_bf(rv[0]) + y[1] * hi_bf(gv[0]);
+                        y[2] = lo_bf(rv[1]) + y[2] * lo_bf(gv[1]);
+                        y[3] = hi_bf(rv[1]) + y[3] * hi_bf(gv[1]);
+                    }
+                    *(u32x2 *)dst = u32x2{pack_bf(y[0], y[1]), pack_bf(y[2], y[3])};
                 }
             }
         }
     }
-    }
 }
 
-#define QW_GEMM_ENTRY(name, EPI, INT8)                                   \
-    QW_KERNEL void __launch_bounds__(256, 1) name(qw_gemm_args a) {      \
-        __shared__ __attribute__((aligned(16))) unsigned char lds[2 * G_LDS_BUF]; \
-        qw_gemm_impl<EPI, INT8>(a, lds);                                  \
+#define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI, PF, FDB)                                 \
+    QW_KERNEL void __launch_bounds__(64 * WM * WN, 1) name(qw_gemm_args a) {                 \
+        __shared__ __attribute__((aligned(16)))                                               \
+            unsigned char lds[(PF == 0 ? 1 : 2) * GemmShape<WM, WN, MI, NI>::STAGE];         \
+        __shared__ __attribute__((aligned(16)))                                               \
+            unsigned char lds_b[PF == 0 ? GemmShape<WM, WN, MI, NI>::STAGE : 16];            \
+        qw_gemm_impl<EPI, INT8, WM, WN, MI, NI, PF, FDB>(a, lds, lds_b);                          \
     }
 
-QW_GEMM_ENTRY(qw_gemm_bf16_store, QW_EPI_STORE, 0)
-QW_GEMM_ENTRY(qw_gemm_bf16_gelu, QW_EPI_GELU, 0)
-QW_GEMM_ENTRY(qw_gemm_bf16_gate, QW_EPI_GATE, 0)
-QW_GEMM_ENTRY(qw_gemm_i8_store, QW_EPI_STORE, 1)
-QW_GEMM_ENTRY(qw_gemm_i8_gelu, QW_EPI_GELU, 1)
-QW_GEMM_ENTRY(qw_gemm_i8_gate, QW_EPI_GATE, 1)
+/* shape A: 4 waves, 128 x 128 per wave */
+#ifndef QW_A_PF
+#define QW_A_PF 0
+#endif
+QW_GEMM_ENTRY(qw_gemm_bf16_store, QW_EPI_STORE, 0, 2, 2, 4, 4, QW_A_PF, 1)
+QW_GEMM_ENTRY(qw_gemm_bf16_gelu, QW_EPI_GELU, 0, 2, 2, 4, 4, QW_A_PF, 1)
+QW_GEMM_ENTRY(qw_gemm_bf16_gate, QW_EPI_GATE, 0, 2, 2, 4, 4, QW_A_PF, 1)
+QW_GEMM_ENTRY(qw_gemm_i8_store, QW_EPI_STORE, 1, 2, 2, 4, 4, QW_A_PF, 1)
+QW_GEMM_ENTRY(qw_gemm_i8_gelu, QW_EPI_GELU, 1, 2, 2, 4, 4, QW_A_PF, 1)
+QW_GEMM_ENTRY(qw_gemm_i8_gate, QW_EPI_GATE, 1, 2, 2, 4, 4, QW_A_PF, 1)
+/* shape B: 8 waves (two per SIMD), 64 x 128 per wave */
+#ifndef QW_W8_PF
+#define QW_W8_PF 1
+#endif
+#ifndef QW_W8_FDB
+#define QW_W8_FDB 1
+#endif
+QW_GEMM_ENTRY(qw_gemm_bf16_store_w8, QW_EPI_STORE, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
+QW_GEMM_ENTRY(qw_gemm_bf16_gelu_w8, QW_EPI_GELU, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
+QW_GEMM_ENTRY(qw_gemm_bf16_gate_w8, QW_EPI_GATE, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
+QW_GEMM_ENTRY(qw_gemm_i8_store_w8, QW_EPI_STORE, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
+QW_GEMM_ENTRY(qw_gemm_i8_gelu_w8, QW_EPI_GELU, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
+QW_GEMM_ENTRY(qw_gemm_i8_gate_w8, QW_EPI_GATE, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)

@@ -27,6 +27,7 @@ typedef struct {
     uint32_t lda, ldc;
     uint32_t gate_row_stride; /* elements between modulation rows */
     uint32_t tiles_m, tiles_n;
+    uint32_t a_bytes, w_bytes; /* buffer-resource extents (< 2^31) */
 } qw_gemm_args;
 
 typedef struct {
