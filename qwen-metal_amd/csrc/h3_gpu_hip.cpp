@@ -17,6 +17,8 @@
 
 #include "../../include/h3_gpu.h"
 #include "../../include/qwen_gpu_ext.h"
+#include <algorithm>
+
 #include "qw_kernel_args.h"
 
 enum {
@@ -25,7 +27,9 @@ enum {
     K_GEMM_BF16_STORE, K_GEMM_BF16_GELU, K_GEMM_BF16_GATE,
     K_GEMM_I8_STORE, K_GEMM_I8_GELU, K_GEMM_I8_GATE,
     K_GEMM_BF16_STORE_W8, K_GEMM_BF16_GELU_W8, K_GEMM_BF16_GATE_W8,
-    K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_COUNT
+    K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8,
+    K_GEMM_BF16_STORE_R, K_GEMM_BF16_GELU_R, K_GEMM_BF16_GATE_R,
+    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_bf16", "qw_rms_norm_one_bf16", "qw_qk_norm_rope_bf16",
@@ -35,7 +39,9 @@ static const char *k_names[K_COUNT] = {
     "qw_gemm_bf16_store", "qw_gemm_bf16_gelu", "qw_gemm_bf16_gate",
     "qw_gemm_i8_store", "qw_gemm_i8_gelu", "qw_gemm_i8_gate",
     "qw_gemm_bf16_store_w8", "qw_gemm_bf16_gelu_w8", "qw_gemm_bf16_gate_w8",
-    "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8"};
+    "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8",
+    "qw_gemm_bf16_store_r", "qw_gemm_bf16_gelu_r", "qw_gemm_bf16_gate_r",
+    "qw_gemm_i8_store_r", "qw_gemm_i8_gelu_r", "qw_gemm_i8_gate_r", "qw_widen_i8_bf16"};
 
 struct h3_gpu {
     int device;
@@ -50,6 +56,8 @@ struct h3_gpu {
     std::string label;
     void *scratch;
     size_t scratch_bytes;
+    void *widen; /* bf16 copy of the int8 weight of the linear in flight */
+    size_t widen_bytes;
 };
 
 struct h3_gpu_tensor {
@@ -139,6 +147,8 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     g->chain_open = 0;
     g->scratch = NULL;
     g->scratch_bytes = 0;
+    g->widen = NULL;
+    g->widen_bytes = 0;
     hipError_t e = hipModuleLoad(&g->module, path.c_str());
     if (e != hipSuccess) {
         set_err(error, error_size, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
@@ -170,6 +180,7 @@ extern "C" void h3_gpu_free(h3_gpu *g) {
     hipSetDevice(g->device);
     hipStreamSynchronize(g->stream);
     if (g->scratch) hipFree(g->scratch);
+    if (g->widen) hipFree(g->widen);
     hipEventDestroy(g->timer0);
     hipEventDestroy(g->timer1);
     hipEventDestroy(g->chain0);
@@ -684,6 +695,9 @@ extern "C" int h3_gpu_copy_bf16(h3_gpu *g, h3_gpu_tensor *dst, size_t doff,
 
 /* ---- GEMM ---------------------------------------------------------------- */
 
+/* below this many rows an int8 linear widens in its GEMM loop instead */
+#define QW_WIDEN_MIN_ROWS 512
+
 extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     if (!g || !d) return 0;
     REQ_DT(d->out, H3_GPU_BF16, "linear out");
@@ -730,9 +744,39 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     } else if (d->epilogue != QW_LINEAR_STORE && d->epilogue != QW_LINEAR_GELU) {
         return fail(g, "linear: unknown epilogue %d", d->epilogue);
     }
+    /* int8 weights with many rows: widen the weight to bf16 once (exact,
+     * unscaled) and run the bf16 GEMM, whose epilogue applies the per-row
+     * scale to the fp32 sums -- the same arithmetic as the int8 kernels,
+     * without their in-loop widening. QW_I8_FUSED=1 keeps the int8 kernels. */
+    static int fused = -1;
+    if (fused < 0) {
+        const char *e = getenv("QW_I8_FUSED");
+        fused = e && e[0] == '1';
+    }
+    const int widen = int8 && !fused && d->rows >= QW_WIDEN_MIN_ROWS;
+    const void *wptr = d->weight->ptr;
+    if (widen) {
+        const size_t n = (size_t)d->cols * d->k, bytes = n * 2;
+        if (g->widen_bytes < bytes) {
+            hipStreamSynchronize(g->stream);
+            if (g->widen) hipFree(g->widen);
+            g->widen = NULL;
+            g->widen_bytes = 0;
+            if (hipMalloc(&g->widen, bytes) != hipSuccess)
+                return fail(g, "linear: widen buffer allocation (%zu bytes) failed", bytes);
+            g->widen_bytes = bytes;
+        }
+        qw_widen_args wa;
+        wa.out = (uint16_t *)g->widen;
+        wa.in = (const int8_t *)d->weight->ptr;
+        wa.count = n; /* k % 64 == 0 */
+        unsigned blocks = (unsigned)std::min<size_t>((n / 16 + 255) / 256, 8192);
+        if (!launch(g, K_WIDEN, dim3(blocks), dim3(256), wa)) return 0;
+        wptr = g->widen;
+    }
     qw_gemm_args a;
     a.a = (const uint16_t *)d->in->ptr + d->in_offset;
-    a.w = d->weight->ptr;
+    a.w = wptr;
     a.wscale = int8 ? (const float *)d->wscale->ptr : NULL;
     a.bias = d->bias ? (const uint16_t *)d->bias->ptr : NULL;
     a.out = (uint16_t *)d->out->ptr + d->out_offset;
@@ -746,24 +790,31 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     a.gate_row_stride = gate_stride;
     {
         const uint64_t ab = ((uint64_t)(d->rows - 1) * d->lda + d->k) * 2;
-        const uint64_t wb = (uint64_t)d->cols * d->k * (int8 ? 1 : 2);
+        const uint64_t wb = (uint64_t)d->cols * d->k * (int8 && !widen ? 1 : 2);
         if (ab >= (1ull << 31) || wb >= (1ull << 31))
             return fail(g, "linear: operand exceeds 2 GiB buffer range");
         a.a_bytes = (uint32_t)ab;
         a.w_bytes = (uint32_t)wb;
     }
-    a.tiles_m = (d->rows + 255) / 256;
-    a.tiles_n = (d->cols + 255) / 256;
-    /* both GEMM shapes cover 256 x 256 per workgroup; QW_GEMM_SHAPE=b
-     * selects the 8-wave variant (two waves per SIMD) */
-    static int shape_b = -1;
-    if (shape_b < 0) {
+    /* kernel family: QW_GEMM_SHAPE = a (256 x 256, 4 waves), b (256 x 256,
+     * 8 waves) or r (128 x 256, 4 waves, two workgroups per CU) */
+    static char shape = 0;
+    if (!shape) {
         const char *e = getenv("QW_GEMM_SHAPE");
-        shape_b = e && e[0] == 'b';
+        shape = (e && (e[0] == 'a' || e[0] == 'b' || e[0] == 'r')) ? e[0] : 'a';
     }
-    int kid = (int8 ? K_GEMM_I8_STORE : K_GEMM_BF16_STORE) + d->epilogue;
-    if (shape_b) kid += K_GEMM_BF16_STORE_W8 - K_GEMM_BF16_STORE;
-    return launch(g, kid, dim3(a.tiles_m * a.tiles_n), dim3(shape_b ? 512 : 256), a);
+    int kid = (int8 && !widen ? K_GEMM_I8_STORE : K_GEMM_BF16_STORE) + d->epilogue;
+    unsigned threads = 256, bm = 256, bn = 256;
+    if (shape == 'b') {
+        kid += K_GEMM_BF16_STORE_W8 - K_GEMM_BF16_STORE;
+        threads = 512;
+    } else if (shape == 'r') {
+        kid += K_GEMM_BF16_STORE_R - K_GEMM_BF16_STORE;
+        bm = 128;
+    }
+    a.tiles_m = (d->rows + bm - 1) / bm;
+    a.tiles_n = (d->cols + bn - 1) / bn;
+    return launch(g, kid, dim3(a.tiles_m * a.tiles_n), dim3(threads), a);
 }
 
 static qw_linear_desc plain_linear(h3_gpu_tensor *out, const h3_gpu_tensor *in,

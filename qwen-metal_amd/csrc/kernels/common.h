@@ -19,13 +19,16 @@ __device__ __forceinline__ float bf2f(u16 b) {
     return __uint_as_float((uint32_t)b << 16);
 }
 
-/* Round-to-nearest-even to bf16 by integer bias (finite inputs), the same
- * rounding as the reference's h3_f32_to_bf16. */
-__device__ __forceinline__ u16 f2bf(float f) {
-    uint32_t b = __float_as_uint(f);
-    b += 0x7fffu + ((b >> 16) & 1u);
-    return (u16)(b >> 16);
+/* Round-to-nearest-even to bf16 (v_cvt_pk_bf16_f32): for finite inputs,
+ * subnormals included, the same rounding as the reference's
+ * h3_f32_to_bf16 (h3_shaders.metal:15: bias 0x7fff + lsb, then
+ * truncate). */
+typedef float qw_f2 __attribute__((ext_vector_type(2)));
+typedef __bf16 qw_b2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(qw_f2{lo, hi}, qw_b2));
 }
+__device__ __forceinline__ u16 f2bf(float f) { return (u16)pack_bf(f, 0.0f); }
 
 __device__ __forceinline__ u16 f2bf_trunc(float f) {
     return (u16)(__float_as_uint(f) >> 16);
@@ -34,9 +37,6 @@ __device__ __forceinline__ u16 f2bf_trunc(float f) {
 /* Low/high bf16 halves of a packed 32-bit word. */
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-__device__ __forceinline__ uint32_t pack_bf(float lo, float hi) {
-    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
-}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -28,10 +28,7 @@
  * lane then holds, for one output row, runs of 4 consecutive output
  * columns, stored as 8-byte writes with the epilogue (scale, bias, GELU,
  * residual gate) applied in registers.
- *
- * Tile order: workgroup ids are dealt round-robin to the 8 XCDs; the id is
- * remapped so each XCD owns a contiguous range of tiles, walked in groups
- * of 8 tile-rows, keeping the A and W panels an XCD touches hot in its L2. */
+ */
 #pragma once
 #include "common.h"
 
@@ -48,21 +45,116 @@ __device__ __forceinline__ uint32_t g_swz(uint32_t row, uint32_t chunk) {
     return row * 128u + ((chunk ^ ((row >> 1) & 7u)) << 4);
 }
 
-/* int8 x16 -> bf16 x16 (exact), as two 16-byte LDS chunks. */
+/* int8 x16 -> bf16 x16 (exact: bf16 holds every 8-bit integer), as two
+ * 16-byte chunks: byte-select conversions to fp32, packed pairwise. */
 __device__ __forceinline__ void i8x16_to_bf16(u32x4 q, u32x4 &lo, u32x4 &hi) {
     uint32_t o[8];
 #pragma unroll
     for (int w = 0; w < 4; w++) {
         int32_t x = (int32_t)q[w];
-        float f0 = (float)((x << 24) >> 24);
-        float f1 = (float)((x << 16) >> 24);
-        float f2 = (float)((x << 8) >> 24);
-        float f3 = (float)(x >> 24);
-        o[2 * w] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-        o[2 * w + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+        o[2 * w] = pack_bf((float)((x << 24) >> 24), (float)((x << 16) >> 24));
+        o[2 * w + 1] = pack_bf((float)((x << 8) >> 24), (float)(x >> 24));
     }
     lo = u32x4{o[0], o[1], o[2], o[3]};
     hi = u32x4{o[4], o[5], o[6], o[7]};
+}
+
+/* out[i] = bf16(q[i]) for count int8 weights (count % 16 == 0): the
+ * unscaled widening that lets int8 linears run on the bf16 GEMM, whose
+ * epilogue then applies the per-row scale to the fp32 sums. */
+QW_KERNEL void __launch_bounds__(256) qw_widen_i8_bf16(qw_widen_args a) {
+    const uint64_t n16 = a.count / 16;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+         i += (uint64_t)gridDim.x * blockDim.x) {
+        u32x4 lo, hi;
+        i8x16_to_bf16(((const u32x4 *)a.in)[i], lo, hi);
+        ((u32x4 *)a.out)[2 * i] = lo;
+        ((u32x4 *)a.out)[2 * i + 1] = hi;
+    }
+}
+
+/* Workgroup id -> (tile row, tile column). Ids are dealt round-robin to the
+ * 8 XCDs; the id is remapped so each XCD owns a contiguous range of tiles,
+ * walked in groups of 8 tile-rows (column-major inside a group), so the A
+ * and W panels an XCD touches stay hot in its L2. */
+__device__ __forceinline__ void gemm_tile(const qw_gemm_args &a, uint32_t &tm, uint32_t &tn) {
+    const uint32_t nt = a.tiles_m * a.tiles_n;
+    uint32_t pid = blockIdx.x;
+    if ((nt & 7u) == 0) pid = (pid & 7u) * (nt >> 3) + (pid >> 3);
+    const uint32_t G = 8;
+    const uint32_t per_group = G * a.tiles_n;
+    const uint32_t first_m = (pid / per_group) * G;
+    const uint32_t gsize = min(a.tiles_m - first_m, G);
+    const uint32_t inner = pid % per_group;
+    tm = first_m + inner % gsize;
+    tn = inner / gsize;
+}
+
+/* Epilogue of one wave's (MI*32) x (NI*32) block of C^T accumulators:
+ * acc[ni][mi][4g + j] = C[row, col] with row = row0 + mi*32 + i32 and
+ * col = col0 + ni*32 + 8g + 4h + j. y = bf16(acc * wscale + bias), then
+ * the epilogue op, written as 8-byte runs of 4 columns. */
+template <int EPI, int INT8, int MI, int NI>
+__device__ __forceinline__ void gemm_epilogue(const qw_gemm_args &a, floatx16 (&acc)[NI][MI],
+                                              uint32_t row0, uint32_t col0, uint32_t h,
+                                              uint32_t i32) {
+#pragma clang fp contract(off)
+    /* int8 weights, or bf16 weights widened from int8 by qw_widen_i8_bf16 */
+    const bool scaled = INT8 || a.wscale != nullptr;
+#ifdef QW_EXP_NO_EPI
+    { /* experiments only: keep the sums live, skip the epilogue */
+        float s = 0.0f;
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int mi = 0; mi < MI; mi++) s += acc[ni][mi][0];
+        if (s != 1234.5f) return;
+    }
+#endif
+#pragma unroll
+    for (int ni = 0; ni < NI; ni++) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const uint32_t col = col0 + ni * 32 + 8 * g + 4 * h;
+            if (col >= a.n) continue; /* n % 8 == 0: a group is all in or out */
+            floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
+            if (scaled) sc = *(const floatx4 *)(a.wscale + col);
+            float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (a.bias) {
+                const u32x2 bb = *(const u32x2 *)(a.bias + col);
+                bias[0] = lo_bf(bb[0]);
+                bias[1] = hi_bf(bb[0]);
+                bias[2] = lo_bf(bb[1]);
+                bias[3] = hi_bf(bb[1]);
+            }
+#pragma unroll
+            for (int mi = 0; mi < MI; mi++) {
+                const uint32_t row = row0 + mi * 32 + i32;
+                if (row >= a.m) continue;
+                float y[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    float t = acc[ni][mi][4 * g + j];
+                    if (scaled) t *= sc[j];
+                    y[j] = bf2f(f2bf(t + bias[j]));
+                }
+                u16 *dst = a.out + (size_t)row * a.ldc + col;
+                if (EPI == QW_EPI_GELU) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) y[j] = gelu_tanh_f(y[j]);
+                } else if (EPI == QW_EPI_GATE) {
+                    const u32x2 gv =
+                        *(const u32x2 *)(a.gate + (size_t)a.row_map[row] * a.gate_row_stride + col);
+                    const u32x2 rv = *(const u32x2 *)dst;
+                    y[0] = lo_bf(rv[0]) + y[0] * lo_bf(gv[0]);
+                    y[1] = hi_bf(rv[0]) + y[1] * hi_bf(gv[0]);
+                    y[2] = lo_bf(rv[1]) + y[2] * lo_bf(gv[1]);
+                    y[3] = hi_bf(rv[1]) + y[3] * hi_bf(gv[1]);
+                }
+                *(u32x2 *)dst = u32x2{pack_bf(y[0], y[1]), pack_bf(y[2], y[3])};
+            }
+        }
+    }
 }
 
 template <int WM, int WN, int MI, int NI>
@@ -188,16 +280,8 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     const uint32_t wm = wave / WN, wn = wave % WN;
     const uint32_t h = lane >> 5, i32 = lane & 31;
 
-    /* ---- tile id -> (tm, tn), XCD-contiguous, grouped by 8 tile-rows ---- */
-    const uint32_t nt = a.tiles_m * a.tiles_n;
-    uint32_t pid = blockIdx.x;
-    if ((nt & 7u) == 0) pid = (pid & 7u) * (nt >> 3) + (pid >> 3);
-    const uint32_t G = 8;
-    const uint32_t per_group = G * a.tiles_n;
-    const uint32_t first_m = (pid / per_group) * G;
-    const uint32_t gsize = min(a.tiles_m - first_m, G);
-    const uint32_t inner = pid % per_group;
-    const uint32_t tm = first_m + inner % gsize, tn = inner / gsize;
+    uint32_t tm, tn;
+    gemm_tile(a, tm, tn);
     const uint32_t m0 = tm * S::BM, n0 = tn * S::BN;
 
     /* ---- global loads: raw buffer loads with 32-bit byte offsets (one
@@ -400,56 +484,7 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
 #undef QW_LOAD
 #undef QW_FRAG
 
-    /* ---- epilogue: acc[ni][mi][4g + j] = C[row, col] with
-     *      row = m0 + wm*MI*32 + mi*32 + i32,
-     *      col = n0 + wn*NI*32 + ni*32 + 8g + 4h + j ----------------------- */
-    {
-#pragma clang fp contract(off)
-#pragma unroll
-        for (int ni = 0; ni < NI; ni++) {
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                const uint32_t col = n0 + wn * (NI * 32) + ni * 32 + 8 * g + 4 * h;
-                if (col >= a.n) continue; /* n % 8 == 0: a group is all in or out */
-                floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
-                if (INT8) sc = *(const floatx4 *)(a.wscale + col);
-                float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (a.bias) {
-                    const u32x2 bb = *(const u32x2 *)(a.bias + col);
-                    bias[0] = lo_bf(bb[0]);
-                    bias[1] = hi_bf(bb[0]);
-                    bias[2] = lo_bf(bb[1]);
-                    bias[3] = hi_bf(bb[1]);
-                }
-#pragma unroll
-                for (int mi = 0; mi < MI; mi++) {
-                    const uint32_t row = m0 + wm * (MI * 32) + mi * 32 + i32;
-                    if (row >= a.m) continue;
-                    float y[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        float t = acc[ni][mi][4 * g + j];
-                        if (INT8) t *= sc[j];
-                        y[j] = bf2f(f2bf(t + bias[j]));
-                    }
-                    u16 *dst = a.out + (size_t)row * a.ldc + col;
-                    if (EPI == QW_EPI_GELU) {
-#pragma unroll
-                        for (int j = 0; j < 4; j++) y[j] = gelu_tanh_f(y[j]);
-                    } else if (EPI == QW_EPI_GATE) {
-                        const u32x2 gv = *(const u32x2 *)(a.gate +
-                                                          (size_t)a.row_map[row] * a.gate_row_stride + col);
-                        const u32x2 rv = *(const u32x2 *)dst;
-                        y[0] = lo_bf(rv[0]) + y[0] * lo_bf(gv[0]);
-                        y[1] = hi_bf(rv[0]) + y[1] * hi_bf(gv[0]);
-                        y[2] = lo_bf(rv[1]) + y[2] * lo_bf(gv[1]);
-                        y[3] = hi_bf(rv[1]) + y[3] * hi_bf(gv[1]);
-                    }
-                    *(u32x2 *)dst = u32x2{pack_bf(y[0], y[1]), pack_bf(y[2], y[3])};
-                }
-            }
-        }
-    }
+    gemm_epilogue<EPI, INT8, MI, NI>(a, acc, m0 + wm * (MI * 32), n0 + wn * (NI * 32), h, i32);
 }
 
 #define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI, PF, FDB)                                 \

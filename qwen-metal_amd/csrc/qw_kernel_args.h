@@ -18,7 +18,8 @@ enum {
 typedef struct {
     const void *a;        /* bf16 [m, k], row stride lda */
     const void *w;        /* bf16 or int8 [n, k], row stride k */
-    const float *wscale;  /* int8: per-row scale [n]; NULL for bf16 */
+    const float *wscale;  /* per-row scale [n]: int8 weights, or bf16 weights
+                           * widened from int8; NULL for plain bf16 */
     const uint16_t *bias; /* bf16 [n] or NULL */
     uint16_t *out;        /* bf16 [m, n], row stride ldc */
     const uint16_t *gate; /* QW_EPI_GATE: modulation base (slot offset applied) */
@@ -110,6 +111,12 @@ typedef struct {
     const uint16_t *w;
     uint32_t rows, cols;
 } qw_quant_args;
+
+typedef struct {
+    uint16_t *out;
+    const int8_t *in;
+    uint64_t count; /* multiple of 16 */
+} qw_widen_args;
 
 typedef struct {
     float *out;

@@ -70,7 +70,9 @@ LINEAR_CASES = [
     (37, 256, 136, True, False),
     (300, 3072, 520, True, False),
     (256, 64, 3072, False, False),
-    (513, 1024, 256, True, True),
+    (513, 1024, 256, True, True),   # int8 widened to bf16 before the GEMM
+    (37, 256, 136, True, True),     # int8 widened inside the GEMM loop
+    (700, 512, 264, False, True),
     (2, 3072, 12288, True, False),
 ]
 
@@ -99,9 +101,9 @@ def test_linear_store(gpu, qd, oracle, rows, k, n, bias, int8):
     assert_linear_close(oracle, got, ref.ravel(), mag)
 
 
-@pytest.mark.parametrize("int8", [False, True])
-def test_linear_gelu_and_gate_epilogues(gpu, qd, oracle, int8):
-    rows, k, n = 300, 512, 768
+@pytest.mark.parametrize("int8,rows", [(False, 300), (True, 300), (True, 600)])
+def test_linear_gelu_and_gate_epilogues(gpu, qd, oracle, int8, rows):
+    k, n = 512, 768
     x = synth(oracle, rows * k, 4)
     w = synth(oracle, n * k, 5, 0.02)
     b = synth(oracle, n, 6, 0.02)
@@ -312,9 +314,17 @@ def test_elementwise_family(gpu, qd, oracle):
     fc1 = synth(oracle, rows * 2 * width, 19, 2.0)
     sw = gpu.new(rows * width, qd.BF16)
     gpu.check(L.qw_gpu_swiglu_bf16(gpu.h, sw.h, gpu.put(fc1).h, rows, width), "swiglu")
-    f = np.random.default_rng(0).standard_normal(999).astype(np.float32)
-    ct = gpu.new(999, qd.BF16)
-    gpu.check(L.h3_gpu_cast_f32_to_bf16(gpu.h, ct.h, gpu.put(f).h, 999), "cast")
+    # rounding cases: normals, random finite bit patterns, subnormals and
+    # exact ties (low 16 bits 0x8000, both parities)
+    rg = np.random.default_rng(0)
+    bits = rg.integers(0, 2**32, 4000, dtype=np.uint64).astype(np.uint32)
+    bits = bits[(bits & 0x7F800000) != 0x7F800000][:1500]
+    sub = (rg.integers(0, 2**23, 500, dtype=np.uint64) | (rg.integers(0, 2, 500, dtype=np.uint64) << 31)).astype(np.uint32)
+    ties = ((rg.integers(0x00800000, 0x7F000000, 500, dtype=np.uint64) & ~np.uint64(0xFFFF)) | 0x8000).astype(np.uint32)
+    f = np.concatenate([rg.standard_normal(999).astype(np.float32), bits.view(np.float32),
+                        sub.view(np.float32), ties.view(np.float32)])
+    ct = gpu.new(f.size, qd.BF16)
+    gpu.check(L.h3_gpu_cast_f32_to_bf16(gpu.h, ct.h, gpu.put(f).h, f.size), "cast")
     gpu.submit()
     ref = np.empty(n, np.uint16)
     OL.qo_gelu_tanh(ref, x, n)
