@@ -11,15 +11,17 @@ inputs are seeded synthetic data generated on the device (no checkpoint).
 
 Timed region: K forward steps (embed, conditioning, 32 blocks, final head)
 with every input already resident in HBM, bracketed by a device sync and
-hipEvents on the library's stream. The dominant kernel (the int8-weight
-up-projection GEMM, M=8704 K=3072 N=12288, GELU epilogue) is timed the same
-way, on the same stream, for the roofline entry; every other linear shape
-and the attention kernel are timed alongside for the breakdown.
+hipEvents on the library's stream. The dominant kernel (the up-projection
+GEMM, M=8704 K=3072 N=12288, GELU epilogue, on the int8 weight widened to
+bf16) is timed the same way, on the same stream, for the roofline entry;
+every other linear shape and the attention kernel are timed alongside for
+the breakdown.
 
 cpu_baseline: the CPU oracle (oracle/, OpenMP) runs ONE of the 32 blocks for
 ONE of the 2 CFG branches at the full 4352-row shape, scaled x64 to a step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       python bench.py --profile-kernel   (launches for rocprofv3 --pmc)
 """
 import argparse
 import json
@@ -72,7 +74,10 @@ def time_ms(gpu, fn, reps):
 
 
 def kernel_breakdown(qd, gpu, reps=10):
-    """Each linear shape of the step and the attention kernel, alone."""
+    """Each linear shape of the step and the attention kernel, alone, on the
+    library's stream. An int8 linear at these rows is two launches: the
+    weight widening (qw_widen_i8_bf16) and the bf16 GEMM with the scale in
+    its epilogue; both are also timed on their own."""
     H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
     L = qd.lib()
     a = gpu.new(M * F, qd.BF16)
@@ -88,12 +93,22 @@ def kernel_breakdown(qd, gpu, reps=10):
         gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, wb.h, 0, n * k, 1, 2, 0.02, 0.0), "fill")
         gpu.check(L.h3_gpu_quantize_weight_int8(gpu.h, q.h, s.h, wb.h, n, k), "quant")
         big = gpu.new(M * n, qd.BF16) if n > 3 * H else out
-        run = lambda: gpu.linear(big, a, q, M, k, n, wscale=s, epilogue=epi)  # noqa: E731
-        run()
-        ms = time_ms(gpu, run, reps)
+        full = lambda: gpu.linear(big, a, q, M, k, n, wscale=s, epilogue=epi)  # noqa: E731
+        widen = lambda: gpu.check(L.qw_gpu_widen_int8_bf16(gpu.h, wb.h, q.h, n * k),  # noqa
+                                  "widen")
+        gemm = lambda: gpu.linear(big, a, wb, M, k, n, wscale=s, epilogue=epi)  # noqa: E731
+        full()
+        ms = time_ms(gpu, full, reps)
+        widen()
+        widen_ms = time_ms(gpu, widen, reps)
+        gemm()
+        gemm_ms = time_ms(gpu, gemm, reps)
         fl = 2.0 * M * n * k
         res[name] = {"M": M, "K": k, "N": n, "ms": ms, "tflops": fl / ms / 1e9,
-                     "frac_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS}
+                     "frac_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS,
+                     "gemm_ms": gemm_ms, "gemm_tflops": fl / gemm_ms / 1e9,
+                     "widen_ms": widen_ms,
+                     "widen_gbs": 3.0 * n * k / widen_ms / 1e6}
         wb.free()
     qkv = gpu.new(M * 3 * H, qd.BF16)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, qkv.h, 0, M * 3 * H, 1, 3, 1.0, 0.0), "fill")
@@ -107,6 +122,20 @@ def kernel_breakdown(qd, gpu, reps=10):
     res["attention"] = {"batch": BATCH, "q_rows": R, "heads": CFG["heads"], "ms": ms,
                         "tflops": sd / ms / 1e9, "frac_peak": sd / ms / 1e9 / PEAK_BF16_TFLOPS}
     return res
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, calibrated against
+    a copy kernel of known size), or None when it has not been measured."""
+    p = os.path.join(ROOT, "profiles", "gemm_up_bf16_gelu_traffic.md")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_launch"):
+                return float(line.split("=")[1])
+    return None
 
 
 def cpu_baseline(blocks=3):
@@ -135,6 +164,30 @@ def cpu_baseline(blocks=3):
                       f"excluded"}
 
 
+def profile_kernel(qd, gpu, reps=5):
+    """Launch-only mode for rocprofv3 --pmc passes: a plain copy of a known
+    size (the counter calibration: 256 MiB read + 256 MiB written), then
+    the dominant GEMM `reps` times. Nothing is timed or printed as a
+    result."""
+    H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
+    L = qd.lib()
+    copy_elems = 128 << 20  # bf16: 256 MiB
+    src, dst = gpu.new(copy_elems, qd.BF16), gpu.new(copy_elems, qd.BF16)
+    for _ in range(3):
+        gpu.check(L.qw_gpu_copy_rows(gpu.h, dst.h, 0, 4096, src.h, 0, 4096,
+                                     copy_elems // 4096, 4096), "copy")
+    a = gpu.new(M * H, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, a.h, 0, M * H, 1, 1, 1.0, 0.0), "fill")
+    wb, q, s = gpu.new(F * H, qd.BF16), gpu.new(F * H, qd.I8), gpu.new(F, qd.F32)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, wb.h, 0, F * H, 1, 2, 0.02, 0.0), "fill")
+    gpu.check(L.h3_gpu_quantize_weight_int8(gpu.h, q.h, s.h, wb.h, F, H), "quant")
+    gpu.check(L.qw_gpu_widen_int8_bf16(gpu.h, wb.h, q.h, F * H), "widen")
+    out = gpu.new(M * F, qd.BF16)
+    for _ in range(reps):
+        gpu.linear(out, a, wb, M, H, F, wscale=s, epilogue=qd.LINEAR_GELU)
+    gpu.submit()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,6 +195,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="only launch a calibration copy and the dominant GEMM (for --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -150,6 +205,10 @@ def main():
 
     qd = load_qdit()
     gpu = qd.Gpu()
+    if args.profile_kernel:
+        profile_kernel(qd, gpu)
+        gpu.close()
+        return
     R, I = TEXT + GH * GW, GH * GW
     L = qd.lib()
     t0 = time.time()
@@ -188,11 +247,13 @@ def main():
     roofline = None
     if up:
         fl = 2.0 * up["M"] * up["N"] * up["K"]
-        achieved = fl / up["ms"] / 1e9
+        achieved = fl / up["gemm_ms"] / 1e9
         roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
-                    "kernel": "qw_gemm_i8_gelu (up-projection, M=8704 K=3072 N=12288)",
-                    "ms_per_launch": up["ms"]}
+                    "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
+                    "traffic": measured_traffic(),
+                    "kernel": "qw_gemm_bf16_gelu (up-projection, M=8704 K=3072 N=12288, "
+                              "int8 weight widened by qw_widen_i8_bf16, scale in the epilogue)",
+                    "flop_per_launch": fl, "ms_per_launch": up["gemm_ms"]}
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": "DiT ms/step @1024^2 (4352 tok, CFG b=2); linear+SDPA TFLOP/s & % MFMA peak",

@@ -94,7 +94,11 @@ enum { QW_LINEAR_STORE = 0, QW_LINEAR_GELU = 1, QW_LINEAR_GATE = 2 };
  *   out = bf16( out + bf16(X W^T * wscale + bias) * gate ) (GATE, in place;
  *         gate row = row_map[r], columns gate_slot*cols..)
  * weight is bf16 [cols, k] or int8 [cols, k] (then wscale f32 [cols] is
- * required). Offsets/strides are in elements; k must be a multiple of 64. */
+ * required; without wscale a bf16 weight is unscaled). Offsets/strides are
+ * in elements; k must be a multiple of 64. An int8 linear of 512 or more
+ * rows first widens the weight to bf16 (qw_gpu_widen_int8_bf16, into a
+ * buffer the runtime keeps) and runs the bf16 GEMM with the scale in its
+ * epilogue: the same sums, the same single rounding. */
 typedef struct {
     h3_gpu_tensor *out;
     size_t out_offset;
@@ -166,6 +170,13 @@ int qw_gpu_dequant_int8_f32(h3_gpu *gpu, h3_gpu_tensor *output,
                             const h3_gpu_tensor *q,
                             const h3_gpu_tensor *scales, uint32_t rows,
                             uint32_t cols);
+
+/* out[i] = bf16(q[i]) for count int8 values (count % 16 == 0): the exact,
+ * unscaled widening used ahead of the bf16 GEMM. No counterpart in the
+ * reference (whose int8 path is h3_shaders.metal:1320-1390 + in-kernel
+ * dequant); exported so callers can keep widened weights resident. */
+int qw_gpu_widen_int8_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
+                           const h3_gpu_tensor *q, size_t count);
 
 /* Strided row copy: rows x row_elems of dtype-size elements. */
 int qw_gpu_copy_rows(h3_gpu *gpu, h3_gpu_tensor *dst, size_t dst_offset,

@@ -37,9 +37,9 @@ extern "C" {
 #define QWEN_ROPE_NEG_ROWS 1024
 #define QWEN_ROPE_ROWS (QWEN_ROPE_POS_ROWS + QWEN_ROPE_NEG_ROWS)
 
-/* reference qwen_host.h:51 */
+/* reference qwen_host.h:50 */
 int qw_latent_grid(int width, int height, int *latent_w, int *latent_h);
-/* reference qwen_host.h:56 */
+/* reference qwen_host.h:55 */
 double qw_calculate_shift(int image_seq_len);
 
 typedef struct {
@@ -47,12 +47,12 @@ typedef struct {
     float sigma[QWEN_MAX_STEPS + 1];
 } qw_sigma_schedule;
 
-/* reference qwen_host.h:67 */
+/* reference qwen_host.h:66 */
 int qw_schedule_build(int steps, int image_seq_len, qw_sigma_schedule *schedule);
-/* reference qwen_host.h:72 */
+/* reference qwen_host.h:70-71 */
 int qw_schedule_from_sigmas(const float *sigmas, int steps,
                             qw_sigma_schedule *schedule);
-/* reference qwen_host.h:77: sample += (sigma - sigma_next) * velocity */
+/* reference qwen_host.h:75-76: sample += (sigma - sigma_next) * velocity */
 void qw_euler_velocity_step(float *sample, const float *velocity,
                             size_t count, float sigma, float sigma_next);
 
@@ -63,7 +63,7 @@ typedef struct {
     float *sin;
 } qw_rope_tables;
 
-/* reference qwen_host.h:93-101 */
+/* reference qwen_host.h:90-97 */
 int qw_rope_build(const int *axis_dim, int axes, qw_rope_tables *tables);
 void qw_rope_free(qw_rope_tables *tables);
 int qw_rope_row(int coordinate);
@@ -75,7 +75,7 @@ typedef struct {
     int has_spare;
 } qw_rng;
 
-/* reference qwen_host.h:103-108 */
+/* reference qwen_host.h:106-109 */
 void qw_rng_seed(qw_rng *rng, uint64_t seed);
 uint32_t qw_rng_u32(qw_rng *rng);
 float qw_rng_normal(qw_rng *rng);

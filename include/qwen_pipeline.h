@@ -28,13 +28,13 @@ typedef struct {
 /* The released base-model scheduler config (dynamic shift, terminal 0.02). */
 void qw_sched_cfg_default(qw_sched_cfg *cfg);
 
-/* reference qwen_pipeline.h:68-72 */
+/* reference qwen_pipeline.h:69-72 */
 int qw_pipe_schedule(uint32_t steps, uint32_t seq_len,
                      const double *turbo_sigmas, uint32_t turbo_count,
                      const qw_sched_cfg *cfg, double *sigmas_out,
                      char *error, size_t error_size);
 
-/* reference qwen_pipeline.h:78-82 */
+/* reference qwen_pipeline.h:78-81 */
 int qw_pipe_rope_tables(h3_gpu *gpu, uint32_t text_rows, uint32_t gh,
                         uint32_t gw, h3_gpu_tensor **rope_cos,
                         h3_gpu_tensor **rope_sin, char *error,
@@ -43,7 +43,7 @@ int qw_pipe_rope_tables(h3_gpu *gpu, uint32_t text_rows, uint32_t gh,
 void qw_pipe_rope_tables_host(uint32_t text_rows, uint32_t gh, uint32_t gw,
                               float *cos_out, float *sin_out);
 
-/* reference qwen_pipeline.h:88-94. latents [gh*gw, 64] fp32 updated in
+/* reference qwen_pipeline.h:87-94. latents [gh*gw, 64] fp32 updated in
  * place. With guidance and neg_rows == text_rows the cond and uncond
  * branches run as ONE batch-2 forward (stacked rows); otherwise as two
  * forwards. */

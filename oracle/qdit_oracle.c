@@ -53,6 +53,13 @@ void qo_f32_to_bf16_array(const float *in, uint16_t *out, size_t n) {
     for (size_t i = 0; i < n; i++) out[i] = rne(in[i]);
 }
 
+/* Attention probability rounding ahead of P.V: 0 = fp32 P (exact
+ * softmax), 1 = P rounded to bf16 after the row sum is taken (the
+ * reference's flash kernel, h3_shaders.metal:2882-3040, multiplies bf16 P
+ * by V). */
+static int g_attn_p_mode = 0;
+void qo_set_attention_p_mode(int mode) { g_attn_p_mode = mode; }
+
 int qo_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();
@@ -329,10 +336,17 @@ static void gemm_chunk(const float *a, size_t lda, const float *b, size_t ldb,
         }
 }
 
+/* K-block of the fp32 contraction: partial sums over KC-wide slices are
+ * added in order. Changing it changes only the fp32 summation order, which
+ * is how the tests measure the rounding-noise band of an implementation
+ * that accumulates in fp32. */
+static size_t g_gemm_kc = 512;
+void qo_set_gemm_kc(size_t kc) { g_gemm_kc = kc ? kc : 512; }
+
 static void gemm_nt_serial(const float *a, size_t lda, const float *b,
                            size_t ldb, float *c, size_t ldc, size_t m,
                            size_t n, size_t k) {
-    const size_t KC = 512;
+    const size_t KC = g_gemm_kc;
     for (size_t k0 = 0; k0 < k || (k == 0 && k0 == 0); k0 += KC) {
         size_t kc = k - k0 < KC ? k - k0 : KC;
         gemm_chunk(a + k0, lda, b + k0, ldb, c, ldc, m, n, kc, k0 > 0);
@@ -658,6 +672,7 @@ void qo_attention(uint16_t *out, size_t ldo, const uint16_t *q, size_t ldq,
                     for (uint32_t j = 0; j < l; j++) {
                         row[j] = expf(row[j] - m);
                         denom += row[j];
+                        if (g_attn_p_mode == 1) row[j] = bf(rne(row[j]));
                     }
                     float invd = denom > 0.0f ? 1.0f / denom : 0.0f;
                     for (uint32_t j = 0; j < l; j++) row[j] *= invd;

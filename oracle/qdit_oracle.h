@@ -233,6 +233,12 @@ int qo_forward(const qo_model *m, const uint16_t *text_in, uint32_t text_rows,
 
 /* Threads used by the OpenMP regions (for the baseline report). */
 int qo_num_threads(void);
+/* 0 (default): fp32 softmax probabilities; 1: probabilities rounded to
+ * bf16 before P.V, as the reference's flash kernel does. */
+void qo_set_attention_p_mode(int mode);
+/* K-slice width of the fp32 contractions (default 512): only the
+ * summation order changes. */
+void qo_set_gemm_kc(size_t kc);
 
 #ifdef __cplusplus
 }

@@ -565,7 +565,10 @@ extern "C" int qw_gpu_qk_norm_rope_bf16(h3_gpu *g, h3_gpu_tensor *qk, uint32_t r
             !fits(rope_sin, 0, (size_t)rope_rows * 64))
             return fail(g, "qk_norm_rope: rope tables too small");
     }
-    if (ld % 2 || k_offset % 2 || k_offset + (size_t)heads * 128 > ld ||
+    if (((uintptr_t)qk->ptr | (do_rope ? (uintptr_t)rope_cos->ptr | (uintptr_t)rope_sin->ptr : 0) |
+         (do_norm ? (uintptr_t)norm_q->ptr | (uintptr_t)norm_k->ptr : 0)) % 16)
+        return fail(g, "qk_norm_rope: tensors must be 16-byte aligned");
+    if (ld % 8 || k_offset % 8 || k_offset + (size_t)heads * 128 > ld ||
         (size_t)heads * 128 > ld || (rows && !fits(qk, 0, (size_t)(rows - 1) * ld + k_offset + heads * 128)))
         return fail(g, "qk_norm_rope: bad geometry");
     qw_qk_norm_rope_args a = {(uint16_t *)qk->ptr,
@@ -576,7 +579,7 @@ extern "C" int qw_gpu_qk_norm_rope_bf16(h3_gpu *g, h3_gpu_tensor *qk, uint32_t r
                               rows, heads, ld, k_offset, do_rope ? rope_rows : 1,
                               do_norm, do_rope, eps};
     uint64_t items = (uint64_t)rows * heads * 2;
-    return launch(g, K_QK_NORM_ROPE, dim3(blocks_for(items, 4)), dim3(256), a);
+    return launch(g, K_QK_NORM_ROPE, dim3(blocks_for(items, 16)), dim3(256), a);
 }
 
 extern "C" int h3_gpu_head_rms_norm_bf16(h3_gpu *g, h3_gpu_tensor *t, const h3_gpu_tensor *w,
@@ -695,6 +698,26 @@ extern "C" int h3_gpu_copy_bf16(h3_gpu *g, h3_gpu_tensor *dst, size_t doff,
 
 /* ---- GEMM ---------------------------------------------------------------- */
 
+static int widen_launch(h3_gpu *g, uint16_t *out, const int8_t *in, size_t n) {
+    qw_widen_args wa;
+    wa.out = out;
+    wa.in = in;
+    wa.count = n;
+    unsigned blocks = (unsigned)std::min<size_t>((n / 16 + 255) / 256, 8192);
+    return launch(g, K_WIDEN, dim3(blocks ? blocks : 1), dim3(256), wa);
+}
+
+extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q,
+                                      size_t count) {
+    if (!g) return 0;
+    REQ_DT(out, H3_GPU_BF16, "widen out");
+    REQ_DT(q, H3_GPU_I8, "widen in");
+    if (count % 16) return fail(g, "widen: count %zu is not a multiple of 16", count);
+    if (!fits(out, 0, count) || !fits(q, 0, count)) return fail(g, "widen: tensor too small");
+    if (!count) return 1;
+    return widen_launch(g, (uint16_t *)out->ptr, (const int8_t *)q->ptr, count);
+}
+
 /* below this many rows an int8 linear widens in its GEMM loop instead */
 #define QW_WIDEN_MIN_ROWS 512
 
@@ -721,8 +744,8 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     if (!fits(d->weight, 0, (size_t)d->cols * d->k)) return fail(g, "linear: weight too small");
     if ((uint64_t)d->cols * d->k >= (1ull << 32) || (uint64_t)d->rows * d->lda >= (1ull << 32))
         return fail(g, "linear: operand exceeds 32-bit element offsets");
-    if (int8) {
-        REQ_DT(d->wscale, H3_GPU_F32, "linear int8 scales");
+    if (int8 || d->wscale) {
+        REQ_DT(d->wscale, H3_GPU_F32, "linear scales");
         if (!fits(d->wscale, 0, d->cols)) return fail(g, "linear: scales too small");
     }
     if (d->bias) {
@@ -766,18 +789,13 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
                 return fail(g, "linear: widen buffer allocation (%zu bytes) failed", bytes);
             g->widen_bytes = bytes;
         }
-        qw_widen_args wa;
-        wa.out = (uint16_t *)g->widen;
-        wa.in = (const int8_t *)d->weight->ptr;
-        wa.count = n; /* k % 64 == 0 */
-        unsigned blocks = (unsigned)std::min<size_t>((n / 16 + 255) / 256, 8192);
-        if (!launch(g, K_WIDEN, dim3(blocks), dim3(256), wa)) return 0;
+        if (!widen_launch(g, (uint16_t *)g->widen, (const int8_t *)d->weight->ptr, n)) return 0;
         wptr = g->widen;
     }
     qw_gemm_args a;
     a.a = (const uint16_t *)d->in->ptr + d->in_offset;
     a.w = wptr;
-    a.wscale = int8 ? (const float *)d->wscale->ptr : NULL;
+    a.wscale = d->wscale ? (const float *)d->wscale->ptr : NULL;
     a.bias = d->bias ? (const uint16_t *)d->bias->ptr : NULL;
     a.out = (uint16_t *)d->out->ptr + d->out_offset;
     a.gate = gate;

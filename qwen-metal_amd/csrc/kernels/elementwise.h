@@ -88,42 +88,61 @@ QW_KERNEL void __launch_bounds__(1024) qw_rms_norm_one_bf16(qw_rms_one_args a) {
 }
 
 /* ---- per-head RMSNorm (single rounding) then interleaved RoPE ----------- */
-/* h3_shaders.metal:4309-4329 followed by 4864-4896, fused: one wave per
- * (row, head, q|k); lane p owns the pair (2p, 2p+1), which is exactly the
- * RoPE pair for table column p. The norm output is rounded to bf16 before
- * the rotation, as the two reference kernels do. In place on a strided
- * [rows, ld] buffer (fused q|k|v projection output). */
+/* h3_shaders.metal:4309-4329 followed by 4864-4896, fused. 16 lanes per
+ * (row, head, q|k) item, 16 items per 256-thread block; lane l owns the 8
+ * elements 8l..8l+7 (one 16-byte load), i.e. the RoPE pairs 4l..4l+3, and
+ * the sum of squares is reduced across the 16 lanes of its item. The norm
+ * output is rounded to bf16 before the rotation, as the two reference
+ * kernels do. In place on a strided [rows, ld] buffer (the fused q|k|v
+ * projection output). */
 QW_KERNEL void __launch_bounds__(256) qw_qk_norm_rope_bf16(qw_qk_norm_rope_args a) {
 #pragma clang fp contract(off)
-    const uint32_t lane = threadIdx.x & 63;
-    const uint64_t item = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t l = threadIdx.x & 15;
+    const uint64_t item = (uint64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
     const uint64_t per_row = 2ull * a.heads;
-    if (item >= (uint64_t)a.rows * per_row) return;
-    const uint32_t row = (uint32_t)(item / per_row);
-    const uint32_t rem = (uint32_t)(item % per_row);
+    const bool active = item < (uint64_t)a.rows * per_row;
+    const uint64_t it = active ? item : 0; /* inactive lanes still join the shuffles */
+    const uint32_t row = (uint32_t)(it / per_row);
+    const uint32_t rem = (uint32_t)(it % per_row);
     const uint32_t is_k = rem >= a.heads;
     const uint32_t head = is_k ? rem - a.heads : rem;
-    u16 *p = a.qk + (size_t)row * a.ld + (is_k ? a.k_offset : 0) + head * QW_HEAD_DIM;
-    uint32_t w2 = *(const uint32_t *)(p + 2 * lane);
-    float x0 = lo_bf(w2), x1 = hi_bf(w2);
+    u16 *p = a.qk + (size_t)row * a.ld + (is_k ? a.k_offset : 0) + head * QW_HEAD_DIM + 8 * l;
+    const u32x4 w = *(const u32x4 *)p;
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        x[2 * i] = lo_bf(w[i]);
+        x[2 * i + 1] = hi_bf(w[i]);
+    }
     if (a.do_norm) {
-        const u16 *nw = is_k ? a.norm_k : a.norm_q;
-        float ss = wave_sum(fmaf(x1, x1, x0 * x0));
-        float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
-        uint32_t wn = *(const uint32_t *)(nw + 2 * lane);
-        x0 = bf2f(f2bf(x0 * inv * lo_bf(wn)));
-        x1 = bf2f(f2bf(x1 * inv * hi_bf(wn)));
+        const u32x4 wn = *(const u32x4 *)((is_k ? a.norm_k : a.norm_q) + 8 * l);
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) ss = fmaf(x[i], x[i], ss);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            x[2 * i] = bf2f(f2bf(x[2 * i] * inv * lo_bf(wn[i])));
+            x[2 * i + 1] = bf2f(f2bf(x[2 * i + 1] * inv * hi_bf(wn[i])));
+        }
     }
     if (a.do_rope) {
-        const uint32_t trow = row % a.rope_rows;
-        float c = a.rope_cos[(size_t)trow * 64 + lane];
-        float s = a.rope_sin[(size_t)trow * 64 + lane];
-        float y0 = x0 * c - x1 * s;
-        float y1 = x0 * s + x1 * c;
-        x0 = y0;
-        x1 = y1;
+        const size_t t = (size_t)(row % a.rope_rows) * 64 + 4 * l;
+        const floatx4 c = *(const floatx4 *)(a.rope_cos + t);
+        const floatx4 sn = *(const floatx4 *)(a.rope_sin + t);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float y0 = x[2 * i] * c[i] - x[2 * i + 1] * sn[i];
+            const float y1 = x[2 * i] * sn[i] + x[2 * i + 1] * c[i];
+            x[2 * i] = y0;
+            x[2 * i + 1] = y1;
+        }
     }
-    *(uint32_t *)(p + 2 * lane) = pack_bf(x0, x1);
+    if (active)
+        *(u32x4 *)p = u32x4{pack_bf(x[0], x[1]), pack_bf(x[2], x[3]), pack_bf(x[4], x[5]),
+                            pack_bf(x[6], x[7])};
 }
 
 /* ---- residual gate: out = res + branch * gate[row_map[r]] ---------------- */

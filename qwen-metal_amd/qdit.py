@@ -124,6 +124,7 @@ SIGNATURES = {
     "qw_gpu_fill_normal_bf16": (C.c_int, [vp, vp, sz, sz, C.c_uint64, C.c_uint64, C.c_float,
                                           C.c_float]),
     "qw_gpu_dequant_int8_f32": (C.c_int, [vp, vp, vp, vp, u32, u32]),
+    "qw_gpu_widen_int8_bf16": (C.c_int, [vp, vp, vp, sz]),
     "qw_gpu_copy_rows": (C.c_int, [vp, vp, sz, u32, vp, sz, u32, u32, u32]),
     "qw_dit_config_reference": (None, [C.POINTER(DitConfig)]),
     "qw_dit_config_baseline": (None, [C.POINTER(DitConfig)]),
