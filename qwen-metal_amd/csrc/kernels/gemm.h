@@ -157,6 +157,96 @@ __device__ __forceinline__ void gemm_epilogue(const qw_gemm_args &a, floatx16 (&
     }
 }
 
+/* Epilogue through LDS: the same arithmetic as gemm_epilogue, but the
+ * fp32 sums of each 32-row slab of the wave's block are first written to a
+ * wave-private LDS region (row stride NI*32 + 4 floats: the 16 lanes of a
+ * ds_write_b128 pass land on 16 distinct 4-bank groups), then read back
+ * row-contiguous: 16 lanes per row, 8 columns (one 16-byte global store)
+ * per lane, so every output row segment is written by whole 256-byte runs
+ * instead of 16-byte pieces, and the residual/gate reads of the GATE
+ * epilogue are coalesced the same way. A lane keeps the same 8 columns for
+ * every row, so it loads their scale and bias once. */
+template <int EPI, int INT8, int MI, int NI>
+__device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx16 (&acc)[NI][MI],
+                                                  float *region, uint32_t row0, uint32_t col0,
+                                                  uint32_t h, uint32_t i32, uint32_t lane) {
+#pragma clang fp contract(off)
+    constexpr uint32_t LDF = NI * 32 + 4; /* floats per staged row */
+    const bool scaled = INT8 || a.wscale != nullptr;
+    /* read-back geometry: lane -> (row within a 4-row group, 8-column chunk) */
+    const uint32_t rr = lane >> 4, cc = lane & 15;
+    constexpr uint32_t CHUNKS = NI * 32 / 8; /* 16 for NI = 4 */
+    static_assert(CHUNKS == 16, "read-back maps 16 lanes to one row");
+    const uint32_t col = col0 + cc * 8;
+    const bool col_ok = col < a.n; /* n % 8 == 0 */
+    float sc[8], bias[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) sc[j] = 1.0f, bias[j] = 0.0f;
+    if (col_ok) {
+        if (scaled) {
+            const floatx4 s0 = *(const floatx4 *)(a.wscale + col);
+            const floatx4 s1 = *(const floatx4 *)(a.wscale + col + 4);
+#pragma unroll
+            for (int j = 0; j < 4; j++) sc[j] = s0[j], sc[4 + j] = s1[j];
+        }
+        if (a.bias) {
+            const u32x4 bb = *(const u32x4 *)(a.bias + col);
+#pragma unroll
+            for (int j = 0; j < 4; j++) bias[2 * j] = lo_bf(bb[j]), bias[2 * j + 1] = hi_bf(bb[j]);
+        }
+    }
+    /* first/second 16-byte halves of the lane's 32 read-back bytes:
+     * lanes 8-15 of a row start with the upper half, so one ds_read_b128
+     * pass covers all 64 banks */
+    const uint32_t swap = (cc >> 3) & 1;
+#pragma unroll
+    for (int mi = 0; mi < MI; mi++) {
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *(floatx4 *)(region + i32 * LDF + ni * 32 + 8 * g + 4 * h) =
+                    floatx4{acc[ni][mi][4 * g], acc[ni][mi][4 * g + 1], acc[ni][mi][4 * g + 2],
+                            acc[ni][mi][4 * g + 3]};
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const uint32_t lr = 4 * p + rr;
+            const floatx4 v0 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * swap);
+            const floatx4 v1 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * (swap ^ 1));
+            const uint32_t row = row0 + mi * 32 + lr;
+            if (!col_ok || row >= a.m) continue;
+            float y[8];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                y[j] = swap ? v1[j] : v0[j];
+                y[4 + j] = swap ? v0[j] : v1[j];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                float t = y[j];
+                if (scaled) t *= sc[j];
+                y[j] = bf2f(f2bf(t + bias[j]));
+            }
+            u16 *dst = a.out + (size_t)row * a.ldc + col;
+            if (EPI == QW_EPI_GELU) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = gelu_tanh_f(y[j]);
+            } else if (EPI == QW_EPI_GATE) {
+                const u32x4 gv =
+                    *(const u32x4 *)(a.gate + (size_t)a.row_map[row] * a.gate_row_stride + col);
+                const u32x4 rv = *(const u32x4 *)dst;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    y[2 * j] = lo_bf(rv[j]) + y[2 * j] * lo_bf(gv[j]);
+                    y[2 * j + 1] = hi_bf(rv[j]) + y[2 * j + 1] * hi_bf(gv[j]);
+                }
+            }
+            *(u32x4 *)dst = u32x4{pack_bf(y[0], y[1]), pack_bf(y[2], y[3]), pack_bf(y[4], y[5]),
+                                  pack_bf(y[6], y[7])};
+        }
+    }
+}
+
 template <int WM, int WN, int MI, int NI>
 struct GemmShape {
     static constexpr int NT = 64 * WM * WN;
@@ -484,6 +574,18 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
 #undef QW_LOAD
 #undef QW_FRAG
 
+#ifndef QW_EXP_NO_EPI
+    if (PF == 0 && WM * WN == 4 && NI == 4) {
+        /* the stages are free after the loop's last barrier: waves 0-1 stage
+         * through `lds`, waves 2-3 through `lds_b` (2 x 16.5 KB each) */
+        static_assert(PF != 0 || WM * WN != 4 || NI != 4 || 2 * 32 * (NI * 32 + 4) * 4 <= S::STAGE,
+                      "epilogue staging exceeds a stage");
+        float *region = (float *)((wave < 2 ? lds : lds_b) + (wave & 1) * (32 * (NI * 32 + 4) * 4));
+        gemm_epilogue_lds<EPI, INT8, MI, NI>(a, acc, region, m0 + wm * (MI * 32),
+                                             n0 + wn * (NI * 32), h, i32, lane);
+        return;
+    }
+#endif
     gemm_epilogue<EPI, INT8, MI, NI>(a, acc, m0 + wm * (MI * 32), n0 + wn * (NI * 32), h, i32);
 }
 
