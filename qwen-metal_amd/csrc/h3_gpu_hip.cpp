@@ -932,6 +932,7 @@ extern "C" int qw_gpu_attention_bf16(h3_gpu *g, const qw_attention_desc *d) {
     a.q_rows = d->q_rows;
     a.kv_rows = d->kv_rows;
     a.heads = d->heads;
+    a.batch = d->batch;
     a.ldq = d->ldq;
     a.ldk = d->ldk;
     a.ldv = d->ldv;
@@ -940,7 +941,9 @@ extern "C" int qw_gpu_attention_bf16(h3_gpu *g, const qw_attention_desc *d) {
     a.text_causal = d->text_causal;
     a.scale_log2 = d->scale * 1.4426950408889634f;
     g->stats.mps_sdpa_dispatches += 0;
-    return launch(g, K_ATTN, dim3((d->q_rows + 127) / 128, d->heads, d->batch), dim3(256), a);
+    const uint64_t nwg = (uint64_t)((d->q_rows + 127) / 128) * d->heads * d->batch;
+    if (nwg >= (1ull << 31)) return fail(g, "attention: grid too large");
+    return launch(g, K_ATTN, dim3((uint32_t)nwg), dim3(256), a);
 }
 
 static int sdpa_contig(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q,

@@ -102,8 +102,14 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
     __shared__ uint32_t lim_red[8];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t h = lane >> 5, j = lane & 31;
-    const uint32_t head = blockIdx.y, b = blockIdx.z;
-    const uint32_t q0 = blockIdx.x * AQB;
+    /* Workgroup ids are dealt round-robin to the 8 XCDs; remap them so
+     * each XCD owns a contiguous range of (batch, head) pairs and all query
+     * blocks of a pair share that XCD's L2 copy of its K and V. */
+    const uint32_t nq = (a.q_rows + AQB - 1) / AQB, nwg = nq * a.heads * a.batch;
+    uint32_t pid = blockIdx.x;
+    if ((nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
+    const uint32_t qblk = pid % nq, head = (pid / nq) % a.heads, b = pid / (nq * a.heads);
+    const uint32_t q0 = qblk * AQB;
     const uint32_t r = q0 + wave * 32 + j; /* this lane's query row */
 
     const u16 *qb = a.q + (size_t)b * a.q_rows * a.ldq + head * 128;
@@ -226,8 +232,12 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
      * clamped or stale tiles whose results nobody reads. */
     auto iter = [&](floatx16 (&sc)[2], floatx16 (&sn)[2], uint32_t t) __attribute__((always_inline)) {
         const uint32_t kv0 = t * AKT;
+#if !defined(QW_AEXP_NOLOAD) && !defined(QW_AEXP_NOK)
         load_k(kv0 + 2 * AKT); /* stored after this tile's math */
+#endif
+#if !defined(QW_AEXP_NOLOAD) && !defined(QW_AEXP_NOV)
         load_v(kv0 + AKT);
+#endif
         if (kv0 + AKT > lmin) attn_mask(sc, kv0, L, h);
 
         qk(lds + ((t + 1) & 1) * A_STAGE, sn);
@@ -243,7 +253,15 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
         const float m_new = mt * c;
         const bool move = m_new > m_run + 8.0f;
         bf16x8 pf[4];
+#ifdef QW_AEXP_NOSOFTMAX
+        float rs = 1.0f;
+#pragma unroll
+        for (int tk = 0; tk < 4; tk++)
+#pragma unroll
+            for (int u = 0; u < 8; u++) pf[tk][u] = (__bf16)sc[tk >> 1][8 * (tk & 1) + u];
+#else
         float rs = attn_exp(sc, pf, c, m_run == -INFINITY ? 0.0f : m_run);
+#endif
         /* QK MFMAs of the next tile with the max/exp VALU and the K
          * fragment reads between them */
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0); /* fragment reads run 2 ahead */
@@ -282,8 +300,20 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
          * (t + 1) % 2 (tile t - 1) are free: every wave passed the barrier
          * that ended the iteration which read them, and this iteration
          * reads only the other two */
+#if !defined(QW_AEXP_NOLOAD) && !defined(QW_AEXP_NOK)
         store_k(t & 1);
+#endif
+#if !defined(QW_AEXP_NOLOAD) && !defined(QW_AEXP_NOV)
+#ifdef QW_AEXP_NOVT
+        {
+            unsigned char *vt = lds + ((t + 1) & 1) * A_STAGE + A_K_BYTES;
+#pragma unroll
+            for (int q = 0; q < 4; q++) *(u32x4 *)(vt + (tid * 4 + q) * 16) = rv[q];
+        }
+#else
         store_v((t + 1) & 1);
+#endif
+#endif
         __syncthreads();
     };
     uint32_t t = 0;

@@ -139,7 +139,7 @@ typedef struct {
     const uint16_t *k;
     const uint16_t *v;
     const uint32_t *kv_limit; /* optional per-query-row limits [q_rows] */
-    uint32_t q_rows, kv_rows, heads;
+    uint32_t q_rows, kv_rows, heads, batch;
     uint32_t ldq, ldk, ldv, ldo; /* row strides in elements */
     uint32_t text_rows;          /* closed-form limits when kv_limit == NULL */
     int32_t text_causal;
