@@ -814,12 +814,13 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
         a.a_bytes = (uint32_t)ab;
         a.w_bytes = (uint32_t)wb;
     }
-    /* kernel family: QW_GEMM_SHAPE = a (256 x 256, 4 waves), b (256 x 256,
-     * 8 waves) or r (128 x 256, 4 waves, two workgroups per CU) */
+    /* kernel family: QW_GEMM_SHAPE = b (default: 256 x 256, 8 waves, two
+     * per SIMD), a (256 x 256, 4 waves) or r (128 x 256, 4 waves, two
+     * workgroups per CU) */
     static char shape = 0;
     if (!shape) {
         const char *e = getenv("QW_GEMM_SHAPE");
-        shape = (e && (e[0] == 'a' || e[0] == 'b' || e[0] == 'r')) ? e[0] : 'a';
+        shape = (e && (e[0] == 'a' || e[0] == 'b' || e[0] == 'r')) ? e[0] : 'b';
     }
     int kid = (int8 && !widen ? K_GEMM_I8_STORE : K_GEMM_BF16_STORE) + d->epilogue;
     unsigned threads = 256, bm = 256, bn = 256;

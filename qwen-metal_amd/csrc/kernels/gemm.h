@@ -575,12 +575,12 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
 #undef QW_FRAG
 
 #ifndef QW_EXP_NO_EPI
-    if (PF == 0 && WM * WN == 4 && NI == 4) {
-        /* the stages are free after the loop's last barrier: waves 0-1 stage
-         * through `lds`, waves 2-3 through `lds_b` (2 x 16.5 KB each) */
-        static_assert(PF != 0 || WM * WN != 4 || NI != 4 || 2 * 32 * (NI * 32 + 4) * 4 <= S::STAGE,
-                      "epilogue staging exceeds a stage");
-        float *region = (float *)((wave < 2 ? lds : lds_b) + (wave & 1) * (32 * (NI * 32 + 4) * 4));
+    if (PF == 0 && NI == 4) {
+        /* the stages are free after the loop's last barrier: the first half
+         * of the waves stage through `lds`, the second through `lds_b`, one
+         * 32-row slab (16.5 KB) per wave at a time */
+        constexpr int NW = WM * WN, REG = 32 * (NI * 32 + 4) * 4;
+        float *region = (float *)((wave < NW / 2 ? lds : lds_b) + (wave % (NW / 2)) * REG);
         gemm_epilogue_lds<EPI, INT8, MI, NI>(a, acc, region, m0 + wm * (MI * 32),
                                              n0 + wn * (NI * 32), h, i32, lane);
         return;
@@ -589,12 +589,21 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     gemm_epilogue<EPI, INT8, MI, NI>(a, acc, m0 + wm * (MI * 32), n0 + wn * (NI * 32), h, i32);
 }
 
+/* LDS of the direct-to-LDS pipeline: two stages, each also large enough
+ * for half of the waves' epilogue slabs */
+template <int WM, int WN, int MI, int NI>
+struct GemmLds {
+    static constexpr int SLABS = WM * WN / 2 * 32 * (NI * 32 + 4) * 4;
+    static constexpr int STAGE = GemmShape<WM, WN, MI, NI>::STAGE;
+    static constexpr int BYTES = STAGE > SLABS ? STAGE : SLABS;
+};
+
 #define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI, PF, FDB)                                 \
     QW_KERNEL void __launch_bounds__(64 * WM * WN, 1) name(qw_gemm_args a) {                 \
+        __shared__ __attribute__((aligned(16))) unsigned char                                \
+            lds[PF == 0 ? GemmLds<WM, WN, MI, NI>::BYTES : 2 * GemmShape<WM, WN, MI, NI>::STAGE]; \
         __shared__ __attribute__((aligned(16)))                                               \
-            unsigned char lds[(PF == 0 ? 1 : 2) * GemmShape<WM, WN, MI, NI>::STAGE];         \
-        __shared__ __attribute__((aligned(16)))                                               \
-            unsigned char lds_b[PF == 0 ? GemmShape<WM, WN, MI, NI>::STAGE : 16];            \
+            unsigned char lds_b[PF == 0 ? GemmLds<WM, WN, MI, NI>::BYTES : 16];              \
         qw_gemm_impl<EPI, INT8, WM, WN, MI, NI, PF, FDB>(a, lds, lds_b);                          \
     }
 
@@ -610,7 +619,7 @@ QW_GEMM_ENTRY(qw_gemm_i8_gelu, QW_EPI_GELU, 1, 2, 2, 4, 4, QW_A_PF, 1)
 QW_GEMM_ENTRY(qw_gemm_i8_gate, QW_EPI_GATE, 1, 2, 2, 4, 4, QW_A_PF, 1)
 /* shape B: 8 waves (two per SIMD), 64 x 128 per wave */
 #ifndef QW_W8_PF
-#define QW_W8_PF 1
+#define QW_W8_PF 0
 #endif
 #ifndef QW_W8_FDB
 #define QW_W8_FDB 1
