@@ -68,11 +68,14 @@ __device__ __forceinline__ float block_sum(float v, float *red) {
  * 0.5 (1 + tanh u) = 1 / (1 + e^(-2u)): one v_exp_f32 and one v_rcp_f32,
  * no cancellation for negative u (the 1 + tanh form loses bits there). */
 __device__ __forceinline__ float gelu_tanh_f(float v) {
-    float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-    if (inner <= -10.0f) return 0.0f;
-    if (inner >= 10.0f) return v;
-    const float e = __builtin_amdgcn_exp2f(inner * -2.8853900817779268f); /* e^(-2u) */
-    return v * __builtin_amdgcn_rcpf(1.0f + e);
+    /* x = -2 u log2(e) = v (C1 + C2 v^2); the reference's saturation
+     * u <= -10 (result +0) is x >= 28.85...; for u >= 10, 1 + 2^x rounds to
+     * 1 and the result is v exactly */
+    const float C1 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+    const float C2 = C1 * 0.044715f;
+    const float x = v * __builtin_fmaf(v * v, C2, C1);
+    const float y = v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x));
+    return x >= 28.853900817779268f ? 0.0f : y;
 }
 
 __device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
