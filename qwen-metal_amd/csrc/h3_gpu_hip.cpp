@@ -29,7 +29,7 @@ enum {
     K_GEMM_BF16_STORE_W8, K_GEMM_BF16_GELU_W8, K_GEMM_BF16_GATE_W8,
     K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8,
     K_GEMM_BF16_STORE_R, K_GEMM_BF16_GELU_R, K_GEMM_BF16_GATE_R,
-    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_COUNT
+    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_bf16", "qw_rms_norm_one_bf16", "qw_qk_norm_rope_bf16",
@@ -41,7 +41,8 @@ static const char *k_names[K_COUNT] = {
     "qw_gemm_bf16_store_w8", "qw_gemm_bf16_gelu_w8", "qw_gemm_bf16_gate_w8",
     "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8",
     "qw_gemm_bf16_store_r", "qw_gemm_bf16_gelu_r", "qw_gemm_bf16_gate_r",
-    "qw_gemm_i8_store_r", "qw_gemm_i8_gelu_r", "qw_gemm_i8_gate_r", "qw_widen_i8_bf16"};
+    "qw_gemm_i8_store_r", "qw_gemm_i8_gelu_r", "qw_gemm_i8_gate_r", "qw_widen_i8_bf16",
+    "qw_layer_norm_mod_wide_bf16"};
 
 struct h3_gpu {
     int device;
@@ -443,7 +444,8 @@ static int ln_mod(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *in,
     qw_ln_mod_args a = {(uint16_t *)out->ptr, (const uint16_t *)in->ptr,
                         (const uint16_t *)mod->ptr, (const uint32_t *)row_map->ptr,
                         rows, width, slots, scale_slot, shift_slot, eps};
-    return launch(g, K_LN_MOD, dim3(rows), dim3((width / 8 + 63) / 64 * 64), a);
+    if (width <= 4096) return launch(g, K_LN_MOD, dim3((rows + 3) / 4), dim3(256), a);
+    return launch(g, K_LN_MOD_WIDE, dim3(rows), dim3((width / 8 + 63) / 64 * 64), a);
 }
 
 extern "C" int qw_gpu_layer_norm_mod_bf16(h3_gpu *g, h3_gpu_tensor *out,

@@ -8,11 +8,73 @@
 #include "common.h"
 
 /* ---- LayerNorm + (1 + scale) [+ shift] --------------------------------- */
-/* h3_shaders.metal:4767-4815. One block per row, width / 8 threads rounded
- * up to whole waves; each thread owns one 16-byte chunk held in registers
- * for both passes (idle tail lanes contribute zeros to the reductions). */
+/* h3_shaders.metal:4767-4815. One wave per row (width <= 4096), four rows
+ * per block: lane l owns the 16-byte chunks l, l + 64, ... of the row,
+ * held in registers for both passes, and both reductions are wave
+ * shuffles (no LDS, no barrier). */
+#define LN_CH 8 /* chunks of 8 per lane: width <= 64 * 8 * 8 = 4096 */
+QW_KERNEL void __launch_bounds__(256) qw_layer_norm_mod_bf16(qw_ln_mod_args a) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.rows) return; /* whole waves */
+    const u16 *in = a.in + (size_t)row * a.width;
+    float x[LN_CH][8];
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < LN_CH; c++) {
+        const uint32_t c8 = (c * 64 + lane) * 8;
+        u32x4 raw = {0, 0, 0, 0};
+        if (c8 < a.width) raw = *(const u32x4 *)(in + c8);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            x[c][2 * i] = lo_bf(raw[i]);
+            x[c][2 * i + 1] = hi_bf(raw[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) s += x[c][i];
+    }
+    const float mean = wave_sum(s) / (float)a.width;
+    float q = 0.0f;
+#pragma unroll
+    for (int c = 0; c < LN_CH; c++) {
+        if ((c * 64 + lane) * 8 >= a.width) continue;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float d = x[c][i] - mean;
+            q = fmaf(d, d, q);
+        }
+    }
+    const float var = wave_sum(q) / (float)a.width;
+    const float inv = 1.0f / sqrtf(var + a.eps);
+    const u16 *mod = a.modulation + (size_t)a.row_map[row] * a.slots * a.width;
+#pragma unroll
+    for (int c = 0; c < LN_CH; c++) {
+        const uint32_t c8 = (c * 64 + lane) * 8;
+        if (c8 >= a.width) continue;
+        const u32x4 sc = *(const u32x4 *)(mod + (size_t)a.scale_slot * a.width + c8);
+        u32x4 sh = {0, 0, 0, 0};
+        if (a.shift_slot >= 0) sh = *(const u32x4 *)(mod + (size_t)a.shift_slot * a.width + c8);
+        u32x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float v0 = ((x[c][2 * i] - mean) * inv) * (1.0f + lo_bf(sc[i]));
+            float v1 = ((x[c][2 * i + 1] - mean) * inv) * (1.0f + hi_bf(sc[i]));
+            if (a.shift_slot >= 0) {
+                v0 += lo_bf(sh[i]);
+                v1 += hi_bf(sh[i]);
+            }
+            o[i] = pack_bf(v0, v1);
+        }
+        *(u32x4 *)(a.out + (size_t)row * a.width + c8) = o;
+    }
+}
+
+/* The same for rows wider than 4096: one block per row, width / 8 threads
+ * rounded up to whole waves, each owning one 16-byte chunk (idle tail
+ * lanes contribute zeros to the reductions). */
 QW_KERNEL void __launch_bounds__(1024)
-qw_layer_norm_mod_bf16(qw_ln_mod_args a) {
+qw_layer_norm_mod_wide_bf16(qw_ln_mod_args a) {
 #pragma clang fp contract(off)
     __shared__ float red[16];
     const uint32_t row = blockIdx.x;

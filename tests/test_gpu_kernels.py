@@ -172,7 +172,7 @@ def test_linear_rejects_bad_shapes(gpu, qd):
         gpu.linear(out, x, w, 64, 64, 128)
 
 
-@pytest.mark.parametrize("width,shift", [(3072, True), (4096, False), (256, True)])
+@pytest.mark.parametrize("width,shift", [(3072, True), (4096, False), (256, True), (6144, True)])
 def test_layer_norm_mod(gpu, qd, oracle, width, shift):
     rows, slots = 129, 6 if shift else 4
     x = synth(oracle, rows * width, 12, 2.0)
