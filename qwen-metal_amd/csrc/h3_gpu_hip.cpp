@@ -944,6 +944,8 @@ extern "C" int qw_gpu_attention_bf16(h3_gpu *g, const qw_attention_desc *d) {
     a.text_causal = d->text_causal;
     a.scale_log2 = d->scale * 1.4426950408889634f;
     g->stats.mps_sdpa_dispatches += 0;
+    if (((uint64_t)(d->kv_rows - 1) * std::max(d->ldk, d->ldv) + hd) * 2 >= (1ull << 31))
+        return fail(g, "attention: one batch entry's K/V exceed 2 GiB");
     const uint64_t nwg = (uint64_t)((d->q_rows + 127) / 128) * d->heads * d->batch;
     if (nwg >= (1ull << 31)) return fail(g, "attention: grid too large");
     return launch(g, K_ATTN, dim3((uint32_t)nwg), dim3(256), a);

@@ -15,11 +15,15 @@
  * Within each 16-key K-step the keys are permuted identically in the V^T
  * (A) and P^T (B) operands, which leaves the contraction unchanged.
  *
- * K tiles (64 keys x 128) and V^T tiles (128 x 64 keys) are staged through
- * LDS, double-buffered, with the next tile's global loads in flight during
- * the current tile's math. Softmax runs in fp32 in the log2 domain (scale *
- * log2 e folded into one FMA before exp2); P is rounded to bf16 for the
- * P.V MFMA and the row sum adds the same rounded values. The running max
+ * K and V tiles (64 keys x 128 d each) go from global memory straight into
+ * LDS (buffer_load ... lds), double-buffered, one tile ahead; V keeps its
+ * row-major layout and the V^T operand is read with the transposing LDS
+ * read of CDNA4 (ds_read_b64_tr_b16), so no register staging, transpose
+ * arithmetic or LDS write instruction touches the operands.
+ *
+ * Softmax runs in fp32 in the log2 domain (scale * log2 e folded into one
+ * FMA before exp2); P is rounded to bf16 for the P.V MFMA and the row sum
+ * adds the same rounded values. The running max
  * is moved lazily (only when a row's tile max exceeds it by 2^8), which
  * keeps O and l consistent while skipping the rescale on most tiles.
  *
@@ -33,11 +37,7 @@
 
 #define AQB 128     /* queries per workgroup (4 waves x 32) */
 #define AKT 64      /* keys per tile */
-#define KS_LD 136   /* K tile row stride (elements) */
-#define VT_LD 72    /* V^T tile row stride (elements) */
-#define A_K_BYTES (AKT * KS_LD * 2)
-#define A_V_BYTES (128 * VT_LD * 2)
-#define A_STAGE (A_K_BYTES + A_V_BYTES)
+#define A_TILE (AKT * 256) /* one K or V tile: 64 keys x 128 bf16 */
 
 __device__ __forceinline__ uint32_t attn_limit(const qw_attn_args &a, uint32_t r) {
     if (r >= a.q_rows) return 0;
@@ -97,10 +97,30 @@ __device__ __forceinline__ void attn_store_rows(const qw_attn_args &a, const flo
         }
 }
 
+/* One 16-byte-per-lane direct load into LDS (buffer_load_dwordx4 ... lds):
+ * M0 = the wave's LDS base, lane l writes base + 16 l. Issued from inline
+ * assembly so the compiler does not treat it as a pending LDS store (it
+ * would wait for every one in flight before each LDS read); the kernel
+ * waits for them itself (vmcnt) before the barrier that publishes a tile. */
+__device__ __forceinline__ void attn_dma(u32x4 rsrc, uint32_t lds_base, uint32_t voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_base), "v"(voff), "s"(rsrc)
+                 : "m0");
+}
+
+__device__ __forceinline__ void attn_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+typedef __attribute__((address_space(3))) bf16x4 attn_lds_b4;
+
 QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
-    __shared__ __attribute__((aligned(16))) unsigned char lds[2 * A_STAGE];
+    /* K stages 0, 1 then V stages 0, 1; 64 keys x 256 B each */
+    __shared__ __attribute__((aligned(16))) unsigned char lds[4 * A_TILE];
     __shared__ uint32_t lim_red[8];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t h = lane >> 5, j = lane & 31;
     /* Workgroup ids are dealt round-robin to the 8 XCDs; remap them so
      * each XCD owns a contiguous range of (batch, head) pairs and all query
@@ -141,106 +161,106 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
         for (int s = 0; s < 8; s++) qf[s] = *(const bf16x8 *)(qrow + 16 * s + 8 * h);
     }
 
-    /* ---- tile loaders ----------------------------------------------------
-     * K: 16 lanes per key row (16 B each), stored row-major (stride KS_LD).
-     * V: lane (vc = tid / 16, vq = 4 (tid % 16)) loads 8 d (chunk vc) of the
-     * 4 keys vq..vq+3 and stores them transposed, 4 keys per 8-byte write
-     * into rows vc*8 + d of V^T. Inside every 16-key group the 4-key
-     * quarters are stored in the order 0, 2, 1, 3, so that the 8 keys an
-     * MFMA lane needs (quarters {0, 2} for k-half 0, {1, 3} for k-half 1,
-     * the key order of the P^T operand) are 16 contiguous bytes. With a
-     * 144-byte row both the writes (two rows 8 apart per pass) and the
-     * 16-byte reads (16 rows per pass) hit distinct banks.
-     * The K tile runs one tile ahead of the V tile (QK of tile t + 1 is
-     * computed while the softmax of tile t runs), so each has its own pair
-     * of stages: K of tile x in stage x % 2, V of tile x in stage x % 2. */
-    const uint32_t kc = tid & 15, kr = tid >> 4; /* K: chunk, key (+16 t) */
-    const uint32_t vc = tid >> 4, vq = (tid & 15) * 4;
-    const uint32_t vcol = (vq & ~15u) | ((((vq >> 2) & 1) << 1 | ((vq >> 3) & 1)) << 2);
-    u32x4 rk[4], rv[4];
-    auto load_k = [&](uint32_t kv0) {
+    floatx16 o[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            uint32_t key = min(kv0 + kr + 16 * t, a.kv_rows - 1);
-            rk[t] = *(const u32x4 *)(kb + (size_t)key * a.ldk + kc * 8);
-        }
-    };
-    auto load_v = [&](uint32_t kv0) {
+    for (int db = 0; db < 4; db++)
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            uint32_t key = min(kv0 + vq + t, a.kv_rows - 1);
-            rv[t] = *(const u32x4 *)(vb + (size_t)key * a.ldv + vc * 8);
-        }
-    };
-    auto store_k = [&](uint32_t buf) {
-        unsigned char *ks = lds + buf * A_STAGE;
+        for (int v = 0; v < 16; v++) o[db][v] = 0.0f;
+
+    /* ---- K / V tiles: 64 keys x 128 d, row-major (256 B rows), straight
+     * from global memory into LDS. 16-byte chunk c of key row k sits at
+     * chunk c ^ (k % 16) in K tiles (the 16 rows of one QK fragment read
+     * pass hit 16 distinct chunks) and at c ^ 4 (k % 4) in V tiles (the 4
+     * rows x 64 B of one transposing read pass hit 16 distinct chunks).
+     * Each wave issues 4 x 1 KB (4 rows) per tile; lane l lands on row
+     * l / 16, physical chunk l % 16, and fetches the logical chunk the
+     * swizzle puts there. */
+    u32x4 rk, rv;
+    {
+        const uint64_t kbase = (uint64_t)kb, vbase = (uint64_t)vb;
+        const uint32_t kbytes = (uint32_t)(((size_t)(a.kv_rows - 1) * a.ldk + 128) * 2);
+        const uint32_t vbytes = (uint32_t)(((size_t)(a.kv_rows - 1) * a.ldv + 128) * 2);
+        rk = u32x4{(uint32_t)kbase, (uint32_t)(kbase >> 32) & 0xffffu, kbytes, 0x00020000u};
+        rv = u32x4{(uint32_t)vbase, (uint32_t)(vbase >> 32) & 0xffffu, vbytes, 0x00020000u};
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)lds;
+    const uint32_t drow = lane >> 4, dphys = lane & 15;
+    auto issue = [&](uint32_t kstage, uint32_t kv0k, uint32_t vstage, uint32_t kv0v)
+        __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-            *(u32x4 *)(ks + ((kr + 16 * t) * KS_LD + kc * 8) * 2) = rk[t];
-    };
-    auto store_v = [&](uint32_t buf) {
-        unsigned char *vt = lds + buf * A_STAGE + A_K_BYTES;
-#pragma unroll
-        for (int d = 0; d < 8; d++) {
-            const uint32_t w = d >> 1;
-            const uint32_t sh = (d & 1) ? 16 : 0;
-            uint32_t k01 = ((rv[0][w] >> sh) & 0xffffu) | (((rv[1][w] >> sh) & 0xffffu) << 16);
-            uint32_t k23 = ((rv[2][w] >> sh) & 0xffffu) | (((rv[3][w] >> sh) & 0xffffu) << 16);
-            *(u32x2 *)(vt + ((vc * 8 + d) * VT_LD + vcol) * 2) = u32x2{k01, k23};
+        for (int jj = 0; jj < 4; jj++) {
+            const uint32_t row = (wave * 4 + jj) * 4 + drow; /* key row in the tile */
+            const uint32_t kk = min(kv0k + row, a.kv_rows - 1);
+            attn_dma(rk, lds0 + kstage * A_TILE + (wave * 4 + jj) * 1024,
+                     (kk * a.ldk + ((dphys ^ (row & 15)) * 8)) * 2);
+            const uint32_t kvv = min(kv0v + row, a.kv_rows - 1);
+            attn_dma(rv, lds0 + (2 + vstage) * A_TILE + (wave * 4 + jj) * 1024,
+                     (kvv * a.ldv + ((dphys ^ (4 * (row & 3))) * 8)) * 2);
         }
     };
     /* S^T of one tile: keys kv0 + [0, 32) and [32, 64) */
-    auto qk = [&](const unsigned char *ks, floatx16 (&s)[2]) {
+    auto qk = [&](uint32_t kstage, floatx16 (&s)[2]) __attribute__((always_inline)) {
+        const unsigned char *ks = lds + kstage * A_TILE;
 #pragma unroll
         for (int kbk = 0; kbk < 2; kbk++) {
 #pragma unroll
             for (int v = 0; v < 16; v++) s[kbk][v] = 0.0f;
 #pragma unroll
             for (int st = 0; st < 8; st++) {
-                const bf16x8 kf =
-                    *(const bf16x8 *)(ks + ((kbk * 32 + j) * KS_LD + 16 * st + 8 * h) * 2);
+                const bf16x8 kf = *(const bf16x8 *)(ks + (kbk * 32 + j) * 256 +
+                                                    (((2 * st + h) ^ (j & 15)) << 4));
                 s[kbk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kbk], 0, 0, 0);
             }
         }
     };
+    /* V^T operand by transposing reads (ds_read_b64_tr_b16): in each 16-lane
+     * group, result lane i element e comes from source lane 4e + i / 4,
+     * element i % 4. Source lane 4e + q reads key row rowbase + e, d =
+     * d_base + 4q..+3, so result lane i holds keys rowbase + 0..3 of column
+     * d_base + i: the A operand of O^T += V^T P^T, in the key order of P^T
+     * (rows 16 tk + 4 h + 0..3, then 16 tk + 8 + 4 h + 0..3). */
+    const uint32_t tq = lane & 3, te = (lane >> 2) & 3;
+    const uint32_t tdb = 16 * ((lane >> 4) & 1) + 4 * tq; /* d offset inside a 32-d block */
+    auto pv = [&](uint32_t vstage, const bf16x8 (&pf)[4]) __attribute__((always_inline)) {
+        const unsigned char *vs = lds + (2 + vstage) * A_TILE;
+#pragma unroll
+        for (int tk = 0; tk < 4; tk++) {
+#pragma unroll
+            for (int db = 0; db < 4; db++) {
+                const uint32_t d = 32 * db + tdb, c = d >> 3, half = (d >> 2) & 1;
+                const uint32_t r0 = 16 * tk + 4 * h + te, r1 = r0 + 8;
+                const bf16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                    (attn_lds_b4 *)(vs + r0 * 256 + ((c ^ (4 * (r0 & 3))) << 4) + half * 8));
+                const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                    (attn_lds_b4 *)(vs + r1 * 256 + ((c ^ (4 * (r1 & 3))) << 4) + half * 8));
+                const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[tk], o[db], 0, 0, 0);
+            }
+        }
+    };
 
-    floatx16 o[4];
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-        for (int v = 0; v < 16; v++) o[db][v] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
     const float c = a.scale_log2;
 
     /* prologue: K(0), V(0), K(1) staged; S(0) computed */
     floatx16 s0[2], s1[2];
     if (ntiles) {
-        load_k(0);
-        load_v(0);
-        store_k(0);
-        store_v(0);
-        load_k(AKT);
-        store_k(1);
+        issue(0, 0, 0, 0);
+        issue(1, AKT, 1, AKT); /* V(1) lands early; harmless */
     }
-    __syncthreads();
-    if (ntiles) qk(lds, s0);
+    __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */
+    attn_barrier();
+    if (ntiles) qk(0, s0);
 
-    /* One tile. Straight-line except the masking of boundary tiles and the
-     * rare running-max move, so the QK MFMAs of tile t + 1 and the softmax
-     * VALU work of tile t share one scheduling region, as do the P.V MFMAs
-     * and the next tiles' LDS stores. Past the end, loads and QK run on
-     * clamped or stale tiles whose results nobody reads. */
+    /* One tile: issue K(t + 2) and V(t + 1) into the stages tile t - 1 used
+     * (their readers passed the previous barrier), QK of tile t + 1, the
+     * softmax and P.V of tile t, then wait for the issued tiles and
+     * barrier. Past the end, loads are clamped and results unused. */
     auto iter = [&](floatx16 (&sc)[2], floatx16 (&sn)[2], uint32_t t) __attribute__((always_inline)) {
         const uint32_t kv0 = t * AKT;
-#if !defined(QW_AEXP_NOLOAD) && !defined(QW_AEXP_NOK)
-        load_k(kv0 + 2 * AKT); /* stored after this tile's math */
-#endif
-#if !defined(QW_AEXP_NOLOAD) && !defined(QW_AEXP_NOV)
-        load_v(kv0 + AKT);
-#endif
+        issue(t & 1, kv0 + 2 * AKT, (t + 1) & 1, kv0 + AKT);
         if (kv0 + AKT > lmin) attn_mask(sc, kv0, L, h);
-
-        qk(lds + ((t + 1) & 1) * A_STAGE, sn);
+        qk((t + 1) & 1, sn);
         float mt = -INFINITY;
 #pragma unroll
         for (int kbk = 0; kbk < 2; kbk++)
@@ -253,24 +273,7 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
         const float m_new = mt * c;
         const bool move = m_new > m_run + 8.0f;
         bf16x8 pf[4];
-#ifdef QW_AEXP_NOSOFTMAX
-        float rs = 1.0f;
-#pragma unroll
-        for (int tk = 0; tk < 4; tk++)
-#pragma unroll
-            for (int u = 0; u < 8; u++) pf[tk][u] = (__bf16)sc[tk >> 1][8 * (tk & 1) + u];
-#else
         float rs = attn_exp(sc, pf, c, m_run == -INFINITY ? 0.0f : m_run);
-#endif
-        /* QK MFMAs of the next tile with the max/exp VALU and the K
-         * fragment reads between them */
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0); /* fragment reads run 2 ahead */
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
-        }
         if (__builtin_amdgcn_ballot_w64(move)) {
             const float m_to = move ? m_new : m_run;
             const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_to);
@@ -284,37 +287,9 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
         }
         rs += __shfl_xor(rs, 32, 64);
         l_run += rs;
-
-        /* O^T += V^T P^T over 4 K-steps of 16 keys */
-        const unsigned char *vt = lds + (t & 1) * A_STAGE + A_K_BYTES;
-#pragma unroll
-        for (int tk = 0; tk < 4; tk++) {
-#pragma unroll
-            for (int db = 0; db < 4; db++) {
-                const bf16x8 vf =
-                    *(const bf16x8 *)(vt + ((db * 32 + j) * VT_LD + 16 * tk + 8 * h) * 2);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[tk], o[db], 0, 0, 0);
-            }
-        }
-        /* K stage t % 2 (tile t, read by last iteration's QK) and V stage
-         * (t + 1) % 2 (tile t - 1) are free: every wave passed the barrier
-         * that ended the iteration which read them, and this iteration
-         * reads only the other two */
-#if !defined(QW_AEXP_NOLOAD) && !defined(QW_AEXP_NOK)
-        store_k(t & 1);
-#endif
-#if !defined(QW_AEXP_NOLOAD) && !defined(QW_AEXP_NOV)
-#ifdef QW_AEXP_NOVT
-        {
-            unsigned char *vt = lds + ((t + 1) & 1) * A_STAGE + A_K_BYTES;
-#pragma unroll
-            for (int q = 0; q < 4; q++) *(u32x4 *)(vt + (tid * 4 + q) * 16) = rv[q];
-        }
-#else
-        store_v((t + 1) & 1);
-#endif
-#endif
-        __syncthreads();
+        pv(t & 1, pf);
+        __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): K(t + 2), V(t + 1) landed */
+        attn_barrier();
     };
     uint32_t t = 0;
     for (; t + 1 < ntiles; t += 2) {
