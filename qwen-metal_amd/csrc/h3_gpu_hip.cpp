@@ -57,6 +57,7 @@ struct h3_gpu {
     std::string label;
     void *scratch;
     size_t scratch_bytes;
+    uint32_t attn_threads; /* attention workgroup size, 64 per 32-query wave */
     void *widen; /* bf16 copy of the int8 weight of the linear in flight */
     size_t widen_bytes;
 };
@@ -165,6 +166,17 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
             return NULL;
         }
     }
+    /* The attention kernel's workgroup (its launch bound) sets the query
+     * block: one 64-lane wave per 32 queries. */
+    int attn_threads = 0;
+    e = hipFuncGetAttribute(&attn_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, g->fn[K_ATTN]);
+    if (e != hipSuccess || attn_threads < 64 || attn_threads > 1024 || attn_threads % 64) {
+        set_err(error, error_size, "qw_attention_bf16: bad workgroup bound %d", attn_threads);
+        hipModuleUnload(g->module);
+        delete g;
+        return NULL;
+    }
+    g->attn_threads = (uint32_t)attn_threads;
     if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&g->timer0) != hipSuccess || hipEventCreate(&g->timer1) != hipSuccess ||
         hipEventCreate(&g->chain0) != hipSuccess || hipEventCreate(&g->chain1) != hipSuccess) {
@@ -946,9 +958,10 @@ extern "C" int qw_gpu_attention_bf16(h3_gpu *g, const qw_attention_desc *d) {
     g->stats.mps_sdpa_dispatches += 0;
     if (((uint64_t)(d->kv_rows - 1) * std::max(d->ldk, d->ldv) + hd) * 2 >= (1ull << 31))
         return fail(g, "attention: one batch entry's K/V exceed 2 GiB");
-    const uint64_t nwg = (uint64_t)((d->q_rows + 127) / 128) * d->heads * d->batch;
+    const uint32_t aqb = g->attn_threads / 2;
+    const uint64_t nwg = (uint64_t)((d->q_rows + aqb - 1) / aqb) * d->heads * d->batch;
     if (nwg >= (1ull << 31)) return fail(g, "attention: grid too large");
-    return launch(g, K_ATTN, dim3((uint32_t)nwg), dim3(256), a);
+    return launch(g, K_ATTN, dim3((uint32_t)nwg), dim3(g->attn_threads), a);
 }
 
 static int sdpa_contig(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *q,

@@ -35,9 +35,11 @@
 #pragma once
 #include "common.h"
 
-#define AQB 128     /* queries per workgroup (4 waves x 32) */
-#define AKT 64      /* keys per tile */
-#define A_TILE (AKT * 256) /* one K or V tile: 64 keys x 128 bf16 */
+#define AKB 2                       /* 32-key blocks per tile */
+#define AKT (32 * AKB)              /* keys per tile */
+#define ANW QW_ATTN_WAVES           /* waves per workgroup, 32 queries each */
+#define AQB (32 * ANW)              /* queries per workgroup */
+#define A_TILE (AKT * 256)          /* one K or V tile: AKT keys x 128 bf16 */
 
 __device__ __forceinline__ uint32_t attn_limit(const qw_attn_args &a, uint32_t r) {
     if (r >= a.q_rows) return 0;
@@ -46,11 +48,11 @@ __device__ __forceinline__ uint32_t attn_limit(const qw_attn_args &a, uint32_t r
     return a.kv_rows;
 }
 
-/* Key of s[kbk][v] in a 64-key tile: kv0 + 32 kbk + 8 (v / 4) + 4 h + v % 4.
+/* Key of s[kbk][v] in a tile: kv0 + 32 kbk + 8 (v / 4) + 4 h + v % 4.
  * Masks keys at or past the row's limit L. */
-__device__ __forceinline__ void attn_mask(floatx16 (&s)[2], uint32_t kv0, uint32_t L, uint32_t h) {
+__device__ __forceinline__ void attn_mask(floatx16 (&s)[AKB], uint32_t kv0, uint32_t L, uint32_t h) {
 #pragma unroll
-    for (int kbk = 0; kbk < 2; kbk++)
+    for (int kbk = 0; kbk < AKB; kbk++)
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             uint32_t key = kv0 + 32 * kbk + 8 * (v >> 2) + 4 * h + (v & 3);
@@ -61,12 +63,12 @@ __device__ __forceinline__ void attn_mask(floatx16 (&s)[2], uint32_t kv0, uint32
 /* P = exp2(S c - m) rounded to bf16 (the B operand of P.V, one bf16x8 per
  * 16-key K-step) and the lane's part of the row sum, which adds the same
  * rounded values (v_dot2 against ones). */
-__device__ __forceinline__ float attn_exp(const floatx16 (&s)[2], bf16x8 (&pf)[4], float c,
-                                          float m_use) {
+__device__ __forceinline__ float attn_exp(const floatx16 (&s)[AKB], bf16x8 (&pf)[2 * AKB],
+                                          float c, float m_use) {
     float rs = 0.0f;
     const qw_b2 ones = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
-    for (int tk = 0; tk < 4; tk++) {
+    for (int tk = 0; tk < 2 * AKB; tk++) {
         const int kbk = tk >> 1, v0 = 8 * (tk & 1);
 #pragma unroll
         for (int u = 0; u < 8; u += 2) {
@@ -115,10 +117,10 @@ __device__ __forceinline__ void attn_barrier() {
 
 typedef __attribute__((address_space(3))) bf16x4 attn_lds_b4;
 
-QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
-    /* K stages 0, 1 then V stages 0, 1; 64 keys x 256 B each */
+QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_args a) {
+    /* K stages 0, 1 then V stages 0, 1; AKT keys x 256 B each */
     __shared__ __attribute__((aligned(16))) unsigned char lds[4 * A_TILE];
-    __shared__ uint32_t lim_red[8];
+    __shared__ uint32_t lim_red[2 * ANW];
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t h = lane >> 5, j = lane & 31;
@@ -146,11 +148,16 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
     }
     if (lane == 0) {
         lim_red[wave] = lmax;
-        lim_red[4 + wave] = lmin;
+        lim_red[ANW + wave] = lmin;
     }
     __syncthreads();
-    lmax = max(max(lim_red[0], lim_red[1]), max(lim_red[2], lim_red[3]));
-    lmin = min(min(lim_red[4], lim_red[5]), min(lim_red[6], lim_red[7]));
+    lmax = 0;
+    lmin = 0xffffffffu;
+#pragma unroll
+    for (int w = 0; w < ANW; w++) {
+        lmax = max(lmax, lim_red[w]);
+        lmin = min(lmin, lim_red[ANW + w]);
+    }
     const uint32_t ntiles = (lmax + AKT - 1) / AKT;
 
     /* ---- Q^T fragments (B operand), resident for the whole loop --------- */
@@ -160,21 +167,22 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
 #pragma unroll
         for (int s = 0; s < 8; s++) qf[s] = *(const bf16x8 *)(qrow + 16 * s + 8 * h);
     }
-
     floatx16 o[4];
 #pragma unroll
     for (int db = 0; db < 4; db++)
 #pragma unroll
         for (int v = 0; v < 16; v++) o[db][v] = 0.0f;
 
-    /* ---- K / V tiles: 64 keys x 128 d, row-major (256 B rows), straight
+    /* ---- K / V tiles: AKT keys x 128 d, row-major (256 B rows), straight
      * from global memory into LDS. 16-byte chunk c of key row k sits at
      * chunk c ^ (k % 16) in K tiles (the 16 rows of one QK fragment read
      * pass hit 16 distinct chunks) and at c ^ 4 (k % 4) in V tiles (the 4
      * rows x 64 B of one transposing read pass hit 16 distinct chunks).
-     * Each wave issues 4 x 1 KB (4 rows) per tile; lane l lands on row
-     * l / 16, physical chunk l % 16, and fetches the logical chunk the
-     * swizzle puts there. */
+     * A direct load covers 1 KB = 4 rows; lane l lands on row l / 16,
+     * physical chunk l % 16, and fetches the logical chunk the swizzle puts
+     * there. */
+    constexpr int DPW = AKT / 4 / ANW; /* direct loads per wave per tile */
+    static_assert(DPW * ANW * 4 == AKT, "K/V tile loads must split evenly over the waves");
     u32x4 rk, rv;
     {
         const uint64_t kbase = (uint64_t)kb, vbase = (uint64_t)vb;
@@ -188,21 +196,22 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
     auto issue = [&](uint32_t kstage, uint32_t kv0k, uint32_t vstage, uint32_t kv0v)
         __attribute__((always_inline)) {
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            const uint32_t row = (wave * 4 + jj) * 4 + drow; /* key row in the tile */
+        for (int jj = 0; jj < DPW; jj++) {
+            const uint32_t blk = wave * DPW + jj;     /* 1 KB block of the tile */
+            const uint32_t row = blk * 4 + drow;      /* key row in the tile */
             const uint32_t kk = min(kv0k + row, a.kv_rows - 1);
-            attn_dma(rk, lds0 + kstage * A_TILE + (wave * 4 + jj) * 1024,
+            attn_dma(rk, lds0 + kstage * A_TILE + blk * 1024,
                      (kk * a.ldk + ((dphys ^ (row & 15)) * 8)) * 2);
             const uint32_t kvv = min(kv0v + row, a.kv_rows - 1);
-            attn_dma(rv, lds0 + (2 + vstage) * A_TILE + (wave * 4 + jj) * 1024,
+            attn_dma(rv, lds0 + (2 + vstage) * A_TILE + blk * 1024,
                      (kvv * a.ldv + ((dphys ^ (4 * (row & 3))) * 8)) * 2);
         }
     };
-    /* S^T of one tile: keys kv0 + [0, 32) and [32, 64) */
-    auto qk = [&](uint32_t kstage, floatx16 (&s)[2]) __attribute__((always_inline)) {
+    /* S^T of one tile: keys kv0 + 32 kbk + [0, 32) */
+    auto qk = [&](uint32_t kstage, floatx16 (&s)[AKB]) __attribute__((always_inline)) {
         const unsigned char *ks = lds + kstage * A_TILE;
 #pragma unroll
-        for (int kbk = 0; kbk < 2; kbk++) {
+        for (int kbk = 0; kbk < AKB; kbk++) {
 #pragma unroll
             for (int v = 0; v < 16; v++) s[kbk][v] = 0.0f;
 #pragma unroll
@@ -221,18 +230,18 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
      * (rows 16 tk + 4 h + 0..3, then 16 tk + 8 + 4 h + 0..3). */
     const uint32_t tq = lane & 3, te = (lane >> 2) & 3;
     const uint32_t tdb = 16 * ((lane >> 4) & 1) + 4 * tq; /* d offset inside a 32-d block */
-    auto pv = [&](uint32_t vstage, const bf16x8 (&pf)[4]) __attribute__((always_inline)) {
+    auto pv = [&](uint32_t vstage, const bf16x8 (&pf)[2 * AKB]) __attribute__((always_inline)) {
         const unsigned char *vs = lds + (2 + vstage) * A_TILE;
 #pragma unroll
-        for (int tk = 0; tk < 4; tk++) {
+        for (int tk = 0; tk < 2 * AKB; tk++) {
 #pragma unroll
             for (int db = 0; db < 4; db++) {
-                const uint32_t d = 32 * db + tdb, c = d >> 3, half = (d >> 2) & 1;
+                const uint32_t d = 32 * db + tdb, cc = d >> 3, half = (d >> 2) & 1;
                 const uint32_t r0 = 16 * tk + 4 * h + te, r1 = r0 + 8;
                 const bf16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                    (attn_lds_b4 *)(vs + r0 * 256 + ((c ^ (4 * (r0 & 3))) << 4) + half * 8));
+                    (attn_lds_b4 *)(vs + r0 * 256 + ((cc ^ (4 * (r0 & 3))) << 4) + half * 8));
                 const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                    (attn_lds_b4 *)(vs + r1 * 256 + ((c ^ (4 * (r1 & 3))) << 4) + half * 8));
+                    (attn_lds_b4 *)(vs + r1 * 256 + ((cc ^ (4 * (r1 & 3))) << 4) + half * 8));
                 const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[tk], o[db], 0, 0, 0);
             }
@@ -241,38 +250,21 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
 
     float m_run = -INFINITY, l_run = 0.0f;
     const float c = a.scale_log2;
-
-    /* prologue: K(0), V(0), K(1) staged; S(0) computed */
-    floatx16 s0[2], s1[2];
-    if (ntiles) {
-        issue(0, 0, 0, 0);
-        issue(1, AKT, 1, AKT); /* V(1) lands early; harmless */
-    }
-    __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */
-    attn_barrier();
-    if (ntiles) qk(0, s0);
-
-    /* One tile: issue K(t + 2) and V(t + 1) into the stages tile t - 1 used
-     * (their readers passed the previous barrier), QK of tile t + 1, the
-     * softmax and P.V of tile t, then wait for the issued tiles and
-     * barrier. Past the end, loads are clamped and results unused. */
-    auto iter = [&](floatx16 (&sc)[2], floatx16 (&sn)[2], uint32_t t) __attribute__((always_inline)) {
-        const uint32_t kv0 = t * AKT;
-        issue(t & 1, kv0 + 2 * AKT, (t + 1) & 1, kv0 + AKT);
+    /* Online-softmax step of a tile whose S is in `sc`: lazy running max
+     * (it moves only when a row's tile max exceeds it by more than 2^8, or
+     * on the first finite max, so p <= 256 and O, l stay consistent; a move
+     * rescales and redoes the tile's P), bf16 P, row sum. */
+    auto softmax = [&](floatx16 (&sc)[AKB], bf16x8 (&pf)[2 * AKB], uint32_t kv0)
+        __attribute__((always_inline)) {
         if (kv0 + AKT > lmin) attn_mask(sc, kv0, L, h);
-        qk((t + 1) & 1, sn);
         float mt = -INFINITY;
 #pragma unroll
-        for (int kbk = 0; kbk < 2; kbk++)
+        for (int kbk = 0; kbk < AKB; kbk++)
 #pragma unroll
             for (int v = 0; v < 16; v++) mt = fmaxf(mt, sc[kbk][v]);
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        /* Lazy running max: it moves only when a row's tile max exceeds it
-         * by more than 2^8 (or on the first finite max), so p <= 256 and O,
-         * l stay consistent; a move rescales and redoes this tile's P. */
         const float m_new = mt * c;
         const bool move = m_new > m_run + 8.0f;
-        bf16x8 pf[4];
         float rs = attn_exp(sc, pf, c, m_run == -INFINITY ? 0.0f : m_run);
         if (__builtin_amdgcn_ballot_w64(move)) {
             const float m_to = move ? m_new : m_run;
@@ -287,6 +279,28 @@ QW_KERNEL void __launch_bounds__(256, 2) qw_attention_bf16(qw_attn_args a) {
         }
         rs += __shfl_xor(rs, 32, 64);
         l_run += rs;
+    };
+
+    /* prologue: K(0), V(0), K(1) staged; S(0) computed */
+    floatx16 s0[AKB], s1[AKB];
+    if (ntiles) {
+        issue(0, 0, 0, 0);
+        issue(1, AKT, 1, AKT); /* V(1) lands early; harmless */
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */
+    attn_barrier();
+    if (ntiles) qk(0, s0);
+    /* One tile: issue K(t + 2) and V(t + 1) into the stages tile t - 1 used
+     * (their readers passed the previous barrier), QK of tile t + 1, the
+     * softmax and P.V of tile t, then wait for the issued tiles and
+     * barrier. Past the end, loads are clamped and results unused. */
+    auto iter = [&](floatx16 (&sc)[AKB], floatx16 (&sn)[AKB], uint32_t t)
+        __attribute__((always_inline)) {
+        const uint32_t kv0 = t * AKT;
+        issue(t & 1, kv0 + 2 * AKT, (t + 1) & 1, kv0 + AKT);
+        qk((t + 1) & 1, sn);
+        bf16x8 pf[2 * AKB];
+        softmax(sc, pf, kv0);
         pv(t & 1, pf);
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): K(t + 2), V(t + 1) landed */
         attn_barrier();

@@ -131,6 +131,12 @@ typedef struct {
     uint64_t rows, row_bytes, dst_stride, src_stride; /* bytes */
 } qw_copy2d_args;
 
+/* Waves per attention workgroup (32 queries each). The host reads the
+ * workgroup size back from the code object. */
+#ifndef QW_ATTN_WAVES
+#define QW_ATTN_WAVES 8
+#endif
+
 /* Flash attention over a joint sequence: out[b*q_rows + r] attends keys
  * [b*kv_rows, b*kv_rows + limit(r)) of the same batch entry. */
 typedef struct {
