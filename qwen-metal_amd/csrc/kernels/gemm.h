@@ -366,7 +366,11 @@ template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int FDB>
 __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned char *lds,
                                              unsigned char *lds_b) {
     typedef GemmShape<WM, WN, MI, NI> S;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    /* wave index in a scalar register: the LDS destinations of the direct
+     * loads (M0) and the fragment bases then need no per-slice
+     * vector-to-scalar moves */
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WN, wn = wave % WN;
     const uint32_t h = lane >> 5, i32 = lane & 31;
 
