@@ -188,6 +188,51 @@ def profile_kernel(qd, gpu, reps=5):
     gpu.submit()
 
 
+def denoise_512(qd, gpu):
+    """the 32-layer DiT (bf16 weights) in the 8-step
+    FlowMatch Euler loop at 512x512 (1024 image + 128 text rows, batch 1,
+    dynamic shift mu = 1), through qw_pipe_denoise. Timed twice: the loop
+    with the latents resident on the device (the default) and the
+    reference's host round trip per step (QW_PIPE_HOST_LOOP=1)."""
+    import ctypes as C
+    L = qd.lib()
+    cfg = dict(CFG, int8_weights=0)
+    text_rows, gh, gw, steps = 128, 32, 32, 8
+    dit = qd.Dit(gpu, cfg, SEED)
+    text = gpu.new(text_rows * cfg["text_dim"], qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, text.h, 0, text.n, SEED, 820, 1.0, 0.0), "fill")
+    rng = np.random.default_rng(SEED)
+    x0 = rng.standard_normal(gh * gw * cfg["z_dim"]).astype(np.float32)
+    # mu = 1: base_shift = max_shift = 1 over an empty sequence range
+
+    class Sched(C.Structure):
+        _fields_ = [("dynamic_shifting", C.c_int), ("base_seq", C.c_double),
+                    ("max_seq", C.c_double), ("base_shift", C.c_double),
+                    ("max_shift", C.c_double), ("has_terminal", C.c_int),
+                    ("shift_terminal", C.c_double)]
+    sc = Sched(1, 256.0, 256.0, 1.0, 1.0, 0, 0.0)
+    res = {}
+    for name, flag in (("device_loop_ms", "0"), ("host_loop_ms", "1")):
+        os.environ["QW_PIPE_HOST_LOOP"] = flag
+        best = None
+        for _ in range(2):
+            x = x0.copy()
+            err = C.create_string_buffer(1024)
+            t = time.time()
+            ok = L.qw_pipe_denoise(dit.h, gpu.h, text.h, text_rows, None, 0, x.ctypes.data, gh,
+                                   gw, steps, 1.0, None, 0, C.byref(sc), err, 1024)
+            ms = (time.time() - t) * 1e3
+            if not ok:
+                raise RuntimeError(err.value.decode())
+            best = ms if best is None else min(best, ms)
+        res[name] = best
+    os.environ.pop("QW_PIPE_HOST_LOOP", None)
+    dit.close()
+    res.update({"steps": steps, "image_rows": gh * gw, "text_rows": text_rows,
+                "weights": "bf16", "latents_finite": bool(np.isfinite(x).all())})
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -254,6 +299,7 @@ def main():
                     "kernel": "qw_gemm_bf16_gelu_w8 (up-projection, M=8704 K=3072 N=12288, "
                               "int8 weight widened by qw_widen_i8_bf16, scale in the epilogue)",
                     "flop_per_launch": fl, "ms_per_launch": up["gemm_ms"]}
+    den = None if args.no_breakdown else denoise_512(qd, gpu)
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": "DiT ms/step @1024^2 (4352 tok, CFG b=2); linear+SDPA TFLOP/s & % MFMA peak",
@@ -269,6 +315,7 @@ def main():
         "step_frac_peak": total_tflops / PEAK_BF16_TFLOPS,
         "flop_per_step": {"linear": lin, "sdpa": sdpa, "other": extra},
         "breakdown": brk,
+        "denoise_512_8step": den,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "wall_ms_per_step": wall_ms / args.steps,

@@ -157,6 +157,18 @@ int qw_dit_forward_batch(qw_dit *dit, const h3_gpu_tensor *text_in,
                          h3_gpu_tensor *output, char *error,
                          size_t error_size);
 
+/* qw_dit_forward_batch with the timestep features read from a device
+ * table: f32 [2, 256] at feature_offset = qw_dit_timestep_features of
+ * {sigma, 0}. No host transfer, so a denoise loop can enqueue every step
+ * without synchronising. No counterpart in the reference. */
+int qw_dit_forward_batch_features(qw_dit *dit, const h3_gpu_tensor *text_in,
+                                  uint32_t text_rows, const h3_gpu_tensor *latents,
+                                  uint32_t image_rows, uint32_t batch,
+                                  const h3_gpu_tensor *features, size_t feature_offset,
+                                  const h3_gpu_tensor *rope_cos,
+                                  const h3_gpu_tensor *rope_sin, h3_gpu_tensor *output,
+                                  char *error, size_t error_size);
+
 /* Per-stage device time of the last qw_dit_forward_batch when
  * QWEN_BLOCK_PROFILE is on (ms summed over layers): input (LN + QKV +
  * norm/rope), attention, to_out+gate, LN2, mlp+gate; plus embed /

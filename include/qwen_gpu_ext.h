@@ -178,6 +178,16 @@ int qw_gpu_dequant_int8_f32(h3_gpu *gpu, h3_gpu_tensor *output,
 int qw_gpu_widen_int8_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                            const h3_gpu_tensor *q, size_t count);
 
+/* One step of the denoise loop on device-resident fp32 latents x[count]:
+ * v = neg ? n + cfg (p - n) : p with p = pos[pos_offset + i],
+ * n = neg[neg_offset + i] (bf16 predictions of the image rows), then
+ * x += dt v; fp32, same operations and rounding points as the host loop
+ * (qwen_pipeline.m:421-429, qw_euler_velocity_step qwen_host.c:372-378).
+ * neg may be NULL (no guidance). */
+int qw_gpu_cfg_euler_f32(h3_gpu *gpu, h3_gpu_tensor *x, const h3_gpu_tensor *pos,
+                         size_t pos_offset, const h3_gpu_tensor *neg,
+                         size_t neg_offset, size_t count, float dt, float cfg);
+
 /* Strided row copy: rows x row_elems of dtype-size elements. */
 int qw_gpu_copy_rows(h3_gpu *gpu, h3_gpu_tensor *dst, size_t dst_offset,
                      uint32_t dst_stride, const h3_gpu_tensor *src,

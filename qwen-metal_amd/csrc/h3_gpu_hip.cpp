@@ -29,7 +29,7 @@ enum {
     K_GEMM_BF16_STORE_W8, K_GEMM_BF16_GELU_W8, K_GEMM_BF16_GATE_W8,
     K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8,
     K_GEMM_BF16_STORE_R, K_GEMM_BF16_GELU_R, K_GEMM_BF16_GATE_R,
-    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_COUNT
+    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_bf16", "qw_rms_norm_one_bf16", "qw_qk_norm_rope_bf16",
@@ -42,7 +42,7 @@ static const char *k_names[K_COUNT] = {
     "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8",
     "qw_gemm_bf16_store_r", "qw_gemm_bf16_gelu_r", "qw_gemm_bf16_gate_r",
     "qw_gemm_i8_store_r", "qw_gemm_i8_gelu_r", "qw_gemm_i8_gate_r", "qw_widen_i8_bf16",
-    "qw_layer_norm_mod_wide_bf16"};
+    "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32"};
 
 struct h3_gpu {
     int device;
@@ -534,6 +534,21 @@ extern "C" int h3_gpu_cast_f32_to_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_g
     if (!fits(out, 0, n) || !fits(in, 0, n)) return fail(g, "cast: tensor too small");
     qw_cast_args a = {(uint16_t *)out->ptr, (const float *)in->ptr, n};
     return launch(g, K_CAST, dim3(blocks_for(n, 256)), dim3(256), a);
+}
+
+extern "C" int qw_gpu_cfg_euler_f32(h3_gpu *g, h3_gpu_tensor *x, const h3_gpu_tensor *pos,
+                                    size_t pos_offset, const h3_gpu_tensor *neg,
+                                    size_t neg_offset, size_t count, float dt, float cfg) {
+    if (!g) return 0;
+    REQ_DT(x, H3_GPU_F32, "euler sample");
+    REQ_DT(pos, H3_GPU_BF16, "euler prediction");
+    if (neg) REQ_DT(neg, H3_GPU_BF16, "euler unconditional prediction");
+    if (!fits(x, 0, count) || !fits(pos, pos_offset, count) ||
+        (neg && !fits(neg, neg_offset, count)))
+        return fail(g, "euler: tensor too small");
+    qw_euler_args a = {(float *)x->ptr, (const uint16_t *)pos->ptr + pos_offset,
+                       neg ? (const uint16_t *)neg->ptr + neg_offset : NULL, count, dt, cfg};
+    return launch(g, K_EULER, dim3(blocks_for(count, 256)), dim3(256), a);
 }
 
 extern "C" int h3_gpu_gate_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *res,

@@ -256,6 +256,19 @@ QW_KERNEL void __launch_bounds__(256) qw_cast_f32_bf16(qw_cast_args a) {
     if (i < a.count) a.out[i] = f2bf(a.in[i]);
 }
 
+/* ---- denoise loop: CFG combine + Euler step, on the resident fp32 latents */
+QW_KERNEL void __launch_bounds__(256) qw_cfg_euler_f32(qw_euler_args a) {
+#pragma clang fp contract(off)
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.count) return;
+    float v = bf2f(a.pos[i]);
+    if (a.neg) {
+        const float n = bf2f(a.neg[i]);
+        v = n + a.cfg * (v - n);
+    }
+    a.x[i] += a.dt * v;
+}
+
 /* ---- conditioning reorder (device replacement of a host round trip) ------ */
 /* qwen_dit.m:1159-1186: scales copied, gates tanh'd in fp32 and stored by
  * truncation (qw_f32_to_bits). Shift variant keeps the shifts in slots 4, 5. */

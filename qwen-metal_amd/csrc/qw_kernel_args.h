@@ -91,6 +91,17 @@ typedef struct {
     uint64_t count;
 } qw_cast_args;
 
+/* Guided Euler step of the denoise loop (qwen_pipeline.m:421-429,
+ * qwen_host.c:372-378): v = neg ? n + cfg (p - n) : p, x += dt v, in fp32
+ * with the host's rounding points (no contraction). */
+typedef struct {
+    float *x;
+    const uint16_t *pos; /* bf16 prediction, image rows */
+    const uint16_t *neg; /* bf16 unconditional prediction or NULL */
+    uint64_t count;
+    float dt, cfg;
+} qw_euler_args;
+
 typedef struct {
     uint16_t *slots_out; /* [mod_rows, S * hidden] */
     const uint16_t *raw;

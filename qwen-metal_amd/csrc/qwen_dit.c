@@ -644,10 +644,13 @@ static int ensure_row_map(qw_dit *d, uint32_t rows, uint32_t text_rows, uint32_t
     return 1;
 }
 
-int qw_dit_forward_batch(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_rows,
-                         const h3_gpu_tensor *latents, uint32_t image_rows, uint32_t batch,
-                         float sigma, const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
-                         h3_gpu_tensor *output, char *error, size_t error_size) {
+/* features: NULL = compute them for {sigma, 0} on the host and upload;
+ * else copy the [2, 256] f32 rows at feat_off of that device table */
+static int forward_impl(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_rows,
+                        const h3_gpu_tensor *latents, uint32_t image_rows, uint32_t batch,
+                        float sigma, const h3_gpu_tensor *features, size_t feat_off,
+                        const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
+                        h3_gpu_tensor *output, char *error, size_t error_size) {
     if (!d) return set_error(error, error_size, "no dit");
     h3_gpu *g = d->gpu;
     const uint32_t rows = text_rows + image_rows, H = d->cfg.hidden, S = slots_of(&d->cfg);
@@ -681,12 +684,17 @@ int qw_dit_forward_batch(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_
     prof_end(d, P_EMBED);
 
     prof_begin(d);
-    const float sigmas[2] = {sigma, 0.0f};
-    float feats[512];
-    qw_dit_timestep_features(sigmas, 2, feats);
-    if (!h3_gpu_tensor_write_f32(d->feat, feats, 512) ||
-        !qw_dit_conditioning(d, d->feat, 2, d->temb, d->modulation, d->norm_out_mod, error,
-                             error_size))
+    int fok;
+    if (features) {
+        fok = qw_gpu_copy_rows(g, d->feat, 0, 512, features, feat_off, 512, 1, 512);
+    } else {
+        const float sigmas[2] = {sigma, 0.0f};
+        float feats[512];
+        qw_dit_timestep_features(sigmas, 2, feats);
+        fok = h3_gpu_tensor_write_f32(d->feat, feats, 512);
+    }
+    if (!fok || !qw_dit_conditioning(d, d->feat, 2, d->temb, d->modulation, d->norm_out_mod,
+                                     error, error_size))
         return error && *error ? 0 : set_error(error, error_size, "conditioning failed");
     prof_end(d, P_COND);
 
@@ -704,6 +712,27 @@ int qw_dit_forward_batch(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_
     (void)S;
     if (!ok) return set_error(error, error_size, "final projection failed: %s", h3_gpu_error(g));
     return 1;
+}
+
+int qw_dit_forward_batch(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_rows,
+                         const h3_gpu_tensor *latents, uint32_t image_rows, uint32_t batch,
+                         float sigma, const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
+                         h3_gpu_tensor *output, char *error, size_t error_size) {
+    return forward_impl(d, text_in, text_rows, latents, image_rows, batch, sigma, NULL, 0,
+                        rope_cos, rope_sin, output, error, error_size);
+}
+
+int qw_dit_forward_batch_features(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_rows,
+                                  const h3_gpu_tensor *latents, uint32_t image_rows,
+                                  uint32_t batch, const h3_gpu_tensor *features,
+                                  size_t feature_offset, const h3_gpu_tensor *rope_cos,
+                                  const h3_gpu_tensor *rope_sin, h3_gpu_tensor *output,
+                                  char *error, size_t error_size) {
+    if (!features || h3_gpu_tensor_dtype(features) != H3_GPU_F32 ||
+        h3_gpu_tensor_elements(features) < feature_offset + 512)
+        return set_error(error, error_size, "features must be f32 [2, 256] at the offset");
+    return forward_impl(d, text_in, text_rows, latents, image_rows, batch, 0.0f, features,
+                        feature_offset, rope_cos, rope_sin, output, error, error_size);
 }
 
 int qw_dit_forward(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_rows,

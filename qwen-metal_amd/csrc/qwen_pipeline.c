@@ -3,6 +3,7 @@
  * With guidance, the cond and uncond branches run as one batch-2 forward
  * (M = 2 * rows in every linear) when their text lengths match. */
 #include "../../include/qwen_pipeline.h"
+#include "../../include/qwen_gpu_ext.h"
 
 #include <math.h>
 #include <stdio.h>
@@ -145,6 +146,65 @@ static float bf16_f32(uint16_t v) {
     return f;
 }
 
+/* The denoise loop with the latents resident on the device (fp32): per step
+ * a bf16 cast (copied for the stacked CFG batch), the forward with its
+ * timestep features from a table uploaded once, and the CFG + Euler kernel
+ * -- no host transfer and no synchronisation until the final read-back. The
+ * arithmetic is the host loop's (qwen_pipeline.m:385-429). */
+static int denoise_device(qw_dit *dit, h3_gpu *gpu, const h3_gpu_tensor *text,
+                          uint32_t text_rows, const h3_gpu_tensor *neg_text_in,
+                          uint32_t neg_rows, float *latents, uint32_t image_rows, uint32_t z,
+                          uint32_t steps, float cfg_scale, const double *sigmas, int guided,
+                          int stacked, const h3_gpu_tensor *cos_t, const h3_gpu_tensor *sin_t,
+                          const h3_gpu_tensor *ncos, const h3_gpu_tensor *nsin,
+                          h3_gpu_tensor *lat, h3_gpu_tensor *pred, h3_gpu_tensor *npred,
+                          char *error, size_t error_size) {
+    const size_t count = (size_t)image_rows * z;
+    const uint32_t rows = text_rows + image_rows;
+    float *ft = malloc(sizeof(float) * 512 * steps);
+    if (!ft) {
+        snprintf(error, error_size, "denoise: out of memory");
+        return 0;
+    }
+    for (uint32_t s = 0; s < steps; s++) {
+        const float sg[2] = {(float)sigmas[s], 0.0f};
+        qw_dit_timestep_features(sg, 2, ft + (size_t)s * 512);
+    }
+    h3_gpu_tensor *x = h3_gpu_tensor_from_f32(gpu, latents, count);
+    h3_gpu_tensor *feat = h3_gpu_tensor_from_f32(gpu, ft, (size_t)512 * steps);
+    free(ft);
+    int ok = x && feat;
+    if (!ok) snprintf(error, error_size, "denoise: allocation failed: %s", h3_gpu_error(gpu));
+    for (uint32_t step = 0; ok && step < steps; step++) {
+        const size_t fo = (size_t)step * 512;
+        const float dt = (float)(sigmas[step + 1] - sigmas[step]);
+        ok = h3_gpu_cast_f32_to_bf16(gpu, lat, x, (uint32_t)count) &&
+             (!stacked || h3_gpu_copy_bf16(gpu, lat, count, lat, 0, count));
+        if (ok && stacked) {
+            ok = qw_dit_forward_batch_features(dit, text, text_rows, lat, image_rows, 2, feat, fo,
+                                               cos_t, sin_t, pred, error, error_size) &&
+                 qw_gpu_cfg_euler_f32(gpu, x, pred, (size_t)text_rows * z, pred,
+                                      (size_t)(rows + text_rows) * z, count, dt, cfg_scale);
+        } else if (ok) {
+            ok = qw_dit_forward_batch_features(dit, text, text_rows, lat, image_rows, 1, feat, fo,
+                                               cos_t, sin_t, pred, error, error_size) &&
+                 (!guided ||
+                  qw_dit_forward_batch_features(dit, neg_text_in, neg_rows, lat, image_rows, 1,
+                                                feat, fo, ncos, nsin, npred, error,
+                                                error_size)) &&
+                 qw_gpu_cfg_euler_f32(gpu, x, pred, (size_t)text_rows * z, guided ? npred : NULL,
+                                      (size_t)neg_rows * z, count, dt, cfg_scale);
+        }
+        if (!ok && error && !*error)
+            snprintf(error, error_size, "denoise step %u: %s", step, h3_gpu_error(gpu));
+    }
+    if (ok) ok = h3_gpu_submit(gpu) && h3_gpu_begin(gpu) && h3_gpu_tensor_read_f32(x, latents, count);
+    if (!ok && error && !*error) snprintf(error, error_size, "denoise: %s", h3_gpu_error(gpu));
+    h3_gpu_tensor_free(x);
+    h3_gpu_tensor_free(feat);
+    return ok;
+}
+
 int qw_pipe_denoise(qw_dit *dit, h3_gpu *gpu, const h3_gpu_tensor *text_in, uint32_t text_rows,
                     const h3_gpu_tensor *neg_text_in, uint32_t neg_rows, float *latents,
                     uint32_t gh, uint32_t gw, uint32_t steps, float cfg_scale,
@@ -194,6 +254,17 @@ int qw_pipe_denoise(qw_dit *dit, h3_gpu *gpu, const h3_gpu_tensor *text_in, uint
         goto done;
     }
     h3_gpu_begin(gpu);
+    const char *hl = getenv("QW_PIPE_HOST_LOOP");
+    if (!(hl && hl[0] == '1')) {
+        ok = denoise_device(dit, gpu, text_rows ? (stacked ? text2 : text_in) : NULL, text_rows,
+                            neg_text_in, neg_rows, latents, image_rows, z, steps, cfg_scale,
+                            sigmas, guided, stacked, cos_t, sin_t, ncos, nsin, lat, pred, npred,
+                            error, error_size);
+        goto done;
+    }
+    /* QW_PIPE_HOST_LOOP=1: the reference's own loop shape, a host round
+     * trip per step (bf16 upload, prediction read-back, CFG + Euler on the
+     * host); kept to check the device loop against */
     for (uint32_t step = 0; ok && step < steps; step++) {
         for (size_t i = 0; i < count; i++) lat_host[i] = bf16_rne(latents[i]);
         if (stacked) memcpy(lat_host + count, lat_host, sizeof(uint16_t) * count);

@@ -125,6 +125,7 @@ SIGNATURES = {
                                           C.c_float]),
     "qw_gpu_dequant_int8_f32": (C.c_int, [vp, vp, vp, vp, u32, u32]),
     "qw_gpu_widen_int8_bf16": (C.c_int, [vp, vp, vp, sz]),
+    "qw_gpu_cfg_euler_f32": (C.c_int, [vp, vp, vp, sz, vp, sz, sz, C.c_float, C.c_float]),
     "qw_gpu_copy_rows": (C.c_int, [vp, vp, sz, u32, vp, sz, u32, u32, u32]),
     "qw_dit_config_reference": (None, [C.POINTER(DitConfig)]),
     "qw_dit_config_baseline": (None, [C.POINTER(DitConfig)]),
@@ -144,6 +145,8 @@ SIGNATURES = {
     "qw_dit_forward": (C.c_int, [vp, vp, u32, vp, u32, C.c_float, vp, vp, vp, C.c_char_p, sz]),
     "qw_dit_forward_batch": (C.c_int, [vp, vp, u32, vp, u32, u32, C.c_float, vp, vp, vp,
                                        C.c_char_p, sz]),
+    "qw_dit_forward_batch_features": (C.c_int, [vp, vp, u32, vp, u32, u32, vp, sz, vp, vp, vp,
+                                                C.c_char_p, sz]),
     "qw_dit_block_profile": (C.c_int, [vp, vp, C.c_int]),
     "qw_latent_grid": (C.c_int, [C.c_int, C.c_int, vp, vp]),
     "qw_calculate_shift": (C.c_double, [C.c_int]),

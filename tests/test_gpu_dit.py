@@ -124,6 +124,62 @@ def test_forward_full_depth_baseline_geometry(gpu, qd, oracle):
         assert cosine(f(got[b][64:]), f(ref[b][64:])) >= 0.9998
 
 
+@pytest.mark.parametrize("case", ["stacked", "unguided", "two_forwards"])
+def test_denoise_loop(gpu, qd, oracle, case, monkeypatch):
+    """qw_pipe_denoise (qwen_pipeline.m:289-486): 3 steps on an 8x8 latent
+    grid with 16 text rows. The default loop keeps the latents on the
+    device; it must equal the host round-trip loop (QW_PIPE_HOST_LOOP=1)
+    bit for bit, and its latent update must match the same loop run on the
+    oracle's forward (CFG combine and Euler step in fp32, numpy) within
+    relL2 2e-2."""
+    import ctypes as C
+    c = cfg("small", int8_weights=0, **BASE_VARIANT)
+    c["layers"] = 2
+    gh = gw = 8
+    I, T, steps = gh * gw, 16, 3
+    cfg_scale, neg_rows = {"stacked": (4.0, 16), "unguided": (1.0, 0),
+                           "two_forwards": (3.0, 8)}[case]
+    text = oracle.fill_normal_bf16(T * c["text_dim"], 5, 910)
+    neg = oracle.fill_normal_bf16(max(neg_rows, 1) * c["text_dim"], 5, 911)
+    x0 = oracle.bf16_to_f32(oracle.fill_normal_bf16(I * c["z_dim"], 5, 912)).astype(np.float32)
+    dit = qd.Dit(gpu, c, 5)
+    L = qd.lib()
+    sched = C.create_string_buffer(256)  # qw_sched_cfg, filled with the released defaults
+    L.qw_sched_cfg_default(sched)
+    tt, nt = gpu.put(text), (gpu.put(neg) if neg_rows else None)
+    runs = []
+    for host_loop in ("0", "1"):
+        monkeypatch.setenv("QW_PIPE_HOST_LOOP", host_loop)
+        x = x0.copy()
+        err = C.create_string_buffer(1024)
+        ok = L.qw_pipe_denoise(dit.h, gpu.h, tt.h, T, nt.h if nt else None, neg_rows,
+                               x.ctypes.data, gh, gw, steps, cfg_scale, None, 0, sched, err, 1024)
+        assert ok, err.value
+        runs.append(x)
+    dit.close()
+    assert np.array_equal(runs[0], runs[1]), "device loop differs from the host loop"
+    # the same loop on the oracle's forward
+    sig = (C.c_double * (steps + 1))()
+    err = C.create_string_buffer(256)
+    assert L.qw_pipe_schedule(steps, I, None, 0, sched, sig, err, 256), err.value
+    om = oracle.Model(c, 5, c["layers"])
+    cos, sin = oracle.rope_tables(T, gh, gw)
+    ncos, nsin = oracle.rope_tables(neg_rows, gh, gw)
+    x = x0.copy()
+    for s in range(steps):
+        lat = oracle.f32_to_bf16(x)
+        p = oracle.bf16_to_f32(om.forward(text, T, lat, I, float(np.float32(sig[s])), cos, sin,
+                                          c["layers"]).reshape(-1, c["z_dim"])[T:]).ravel()
+        if cfg_scale > 1.0:
+            n = oracle.bf16_to_f32(om.forward(neg, neg_rows, lat, I, float(np.float32(sig[s])),
+                                              ncos, nsin, c["layers"])
+                                   .reshape(-1, c["z_dim"])[neg_rows:]).ravel()
+            p = (n + np.float32(cfg_scale) * (p - n)).astype(np.float32)
+        x = (x + np.float32(sig[s + 1] - sig[s]) * p).astype(np.float32)
+    om.close()
+    assert rel_l2(runs[0] - x0, x - x0) < 2e-2
+
+
 def test_forward_no_text_rows(gpu, qd, oracle):
     """dit_fixture case a topology: image rows only."""
     c = cfg("small", **REF_VARIANT)
