@@ -60,6 +60,9 @@ struct h3_gpu {
     uint32_t attn_threads; /* attention workgroup size, 64 per 32-query wave */
     void *widen; /* bf16 copy of the int8 weight of the linear in flight */
     size_t widen_bytes;
+    uint32_t cus;      /* compute units */
+    float *sk_part;    /* split-tile partials: 256 x 256 fp32 each */
+    uint32_t *sk_flag; /* split-tile piece counters, 0 between launches */
 };
 
 struct h3_gpu_tensor {
@@ -151,6 +154,9 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     g->scratch_bytes = 0;
     g->widen = NULL;
     g->widen_bytes = 0;
+    g->cus = 0;
+    g->sk_part = NULL;
+    g->sk_flag = NULL;
     hipError_t e = hipModuleLoad(&g->module, path.c_str());
     if (e != hipSuccess) {
         set_err(error, error_size, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
@@ -177,6 +183,15 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
         return NULL;
     }
     g->attn_threads = (uint32_t)attn_threads;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, g->device) != hipSuccess ||
+        cus <= 0) {
+        set_err(error, error_size, "compute unit count unavailable");
+        hipModuleUnload(g->module);
+        delete g;
+        return NULL;
+    }
+    g->cus = (uint32_t)cus;
     if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&g->timer0) != hipSuccess || hipEventCreate(&g->timer1) != hipSuccess ||
         hipEventCreate(&g->chain0) != hipSuccess || hipEventCreate(&g->chain1) != hipSuccess) {
@@ -194,6 +209,8 @@ extern "C" void h3_gpu_free(h3_gpu *g) {
     hipStreamSynchronize(g->stream);
     if (g->scratch) hipFree(g->scratch);
     if (g->widen) hipFree(g->widen);
+    if (g->sk_part) hipFree(g->sk_part);
+    if (g->sk_flag) hipFree(g->sk_flag);
     hipEventDestroy(g->timer0);
     hipEventDestroy(g->timer1);
     hipEventDestroy(g->chain0);
@@ -750,6 +767,45 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
 /* below this many rows an int8 linear widens in its GEMM loop instead */
 #define QW_WIDEN_MIN_ROWS 512
 
+/* Split tiles. A grid of one workgroup per 256 x 256 tile runs in waves of
+ * `cus` tiles; when the last wave is partly filled (R = tiles % cus tiles,
+ * all of them when there is no full wave), each of its tiles can instead be
+ * cut into s k-ranges: R s pieces taking ceil(R s / cus) waves of 1/s the
+ * length. s minimises that tail time plus 0.02 (s - 1) for writing and
+ * re-reading the fp32 partials, and is used only when that beats 0.9 of the
+ * whole-tile tail. Pieces stay at least 32 k-steps (2048 k) long: shorter
+ * pieces lost more to their partials than they gained (K = 3072 linears
+ * measured slower when split, K = 12288 ones faster), and
+ * R s <= QW_SPLIT_MAX_PIECES * cus bounds the partial workspace.
+ * QW_GEMM_SPLIT=0 (or 1) disables it, =N forces s = N where allowed. */
+#define QW_SPLIT_MAX_PIECES 2
+static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps) {
+    static int mode = -1;
+    if (mode < 0) {
+        const char *e = getenv("QW_GEMM_SPLIT");
+        mode = e ? atoi(e) : 9999; /* 9999: automatic */
+        if (mode < 0) mode = 0;
+    }
+    if (mode <= 1) return 1;
+    const uint32_t G = g->cus, R = tiles % G;
+    if (R == 0) return 1;
+    uint32_t best = 1;
+    double best_t = 0.9;
+    for (uint32_t s = 2; s <= 8; s++) {
+        if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * G || ksteps < 32 * s) break;
+        if (mode != 9999) {
+            if (s == (uint32_t)mode) return s;
+            continue;
+        }
+        const double t = (double)((R * s + G - 1) / G) / s + 0.02 * (s - 1);
+        if (t < best_t) {
+            best_t = t;
+            best = s;
+        }
+    }
+    return mode != 9999 ? 1 : best;
+}
+
 extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     if (!g || !d) return 0;
     REQ_DT(d->out, H3_GPU_BF16, "linear out");
@@ -862,7 +918,39 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     }
     a.tiles_m = (d->rows + bm - 1) / bm;
     a.tiles_n = (d->cols + bn - 1) / bn;
-    return launch(g, kid, dim3(a.tiles_m * a.tiles_n), dim3(threads), a);
+    const uint32_t tiles = a.tiles_m * a.tiles_n;
+    a.dp_tiles = tiles;
+    a.split = 1;
+    a.sk_part = NULL;
+    a.sk_flag = NULL;
+    uint32_t grid = tiles;
+    if (shape != 'r') {
+        const uint32_t s = split_choice(g, tiles, d->k / 64);
+        if (s > 1) {
+            if (!g->sk_part) {
+                hipStreamSynchronize(g->stream);
+                const size_t n = (size_t)QW_SPLIT_MAX_PIECES * g->cus;
+                if (hipMalloc((void **)&g->sk_part, n * 256 * 256 * 4) != hipSuccess) {
+                    g->sk_part = NULL;
+                    return fail(g, "linear: split-tile workspace allocation failed");
+                }
+                if (hipMalloc((void **)&g->sk_flag, (size_t)g->cus * 4) != hipSuccess ||
+                    hipMemset(g->sk_flag, 0, (size_t)g->cus * 4) != hipSuccess) {
+                    hipFree(g->sk_part);
+                    g->sk_part = NULL;
+                    g->sk_flag = NULL;
+                    return fail(g, "linear: split-tile flag allocation failed");
+                }
+            }
+            const uint32_t R = tiles % g->cus;
+            a.dp_tiles = tiles - R;
+            a.split = s;
+            a.sk_part = g->sk_part;
+            a.sk_flag = g->sk_flag;
+            grid = a.dp_tiles + R * s;
+        }
+    }
+    return launch(g, kid, dim3(grid), dim3(threads), a);
 }
 
 static qw_linear_desc plain_linear(h3_gpu_tensor *out, const h3_gpu_tensor *in,

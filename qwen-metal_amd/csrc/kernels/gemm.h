@@ -33,6 +33,10 @@
 #include "common.h"
 
 #define GBK 64
+/* floats per split-tile partial (one 256 x 256 tile) */
+#define QW_SPLIT_PART (256u * 256u)
+/* buffer cache policy sc0 | sc1: coherent at device scope */
+#define QW_CPOL_COHERENT 17
 /* QW_EXP_FIXED_K (experiments only, never in the shipped build): every
  * K-slice load re-reads slice 0, isolating global-memory effects. */
 #ifdef QW_EXP_FIXED_K
@@ -77,10 +81,8 @@ QW_KERNEL void __launch_bounds__(256) qw_widen_i8_bf16(qw_widen_args a) {
  * 8 XCDs; the id is remapped so each XCD owns a contiguous range of tiles,
  * walked in groups of 8 tile-rows (column-major inside a group), so the A
  * and W panels an XCD touches stay hot in its L2. */
-__device__ __forceinline__ void gemm_tile(const qw_gemm_args &a, uint32_t &tm, uint32_t &tn) {
-    const uint32_t nt = a.tiles_m * a.tiles_n;
-    uint32_t pid = blockIdx.x;
-    if ((nt & 7u) == 0) pid = (pid & 7u) * (nt >> 3) + (pid >> 3);
+__device__ __forceinline__ void gemm_tile_at(const qw_gemm_args &a, uint32_t pid, uint32_t &tm,
+                                             uint32_t &tn) {
     const uint32_t G = 8;
     const uint32_t per_group = G * a.tiles_n;
     const uint32_t first_m = (pid / per_group) * G;
@@ -88,6 +90,12 @@ __device__ __forceinline__ void gemm_tile(const qw_gemm_args &a, uint32_t &tm, u
     const uint32_t inner = pid % per_group;
     tm = first_m + inner % gsize;
     tn = inner / gsize;
+}
+__device__ __forceinline__ void gemm_tile(const qw_gemm_args &a, uint32_t &tm, uint32_t &tn) {
+    const uint32_t nt = a.tiles_m * a.tiles_n;
+    uint32_t pid = blockIdx.x;
+    if ((nt & 7u) == 0) pid = (pid & 7u) * (nt >> 3) + (pid >> 3);
+    gemm_tile_at(a, pid, tm, tn);
 }
 
 /* Epilogue of one wave's (MI*32) x (NI*32) block of C^T accumulators:
@@ -169,10 +177,17 @@ __device__ __forceinline__ void gemm_epilogue(const qw_gemm_args &a, floatx16 (&
 template <int EPI, int INT8, int MI, int NI>
 __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx16 (&acc)[NI][MI],
                                                   float *region, uint32_t row0, uint32_t col0,
-                                                  uint32_t h, uint32_t i32, uint32_t lane) {
+                                                  uint32_t h, uint32_t i32, uint32_t lane,
+                                                  float *pst, const float *pld, uint32_t npart,
+                                                  uint32_t own) {
 #pragma clang fp contract(off)
     constexpr uint32_t LDF = NI * 32 + 4; /* floats per staged row */
     const bool scaled = INT8 || a.wscale != nullptr;
+    /* split-tile partials go through device-coherent buffer accesses (write
+     * through / read past the XCD's L2), so pieces on different XCDs see
+     * each other's sums without any L2 write-back or invalidate */
+    const __amdgpu_buffer_rsrc_t part_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)a.sk_part, (short)0, (int)0x7FFFFFF0, 0x00020000);
     /* read-back geometry: lane -> (row within a 4-row group, 8-column chunk) */
     const uint32_t rr = lane >> 4, cc = lane & 15;
     constexpr uint32_t CHUNKS = NI * 32 / 8; /* 16 for NI = 4 */
@@ -220,6 +235,41 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx1
             for (int j = 0; j < 4; j++) {
                 y[j] = swap ? v1[j] : v0[j];
                 y[4 + j] = swap ? v0[j] : v1[j];
+            }
+            const uint32_t poff = (mi * 32 + lr) * 256 + cc * 8;
+            if (pst) { /* piece of a split tile: keep the fp32 sums */
+                const uint32_t bo = (uint32_t)((pst - a.sk_part) + poff) * 4;
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4, floatx4{y[0], y[1], y[2], y[3]}), part_rsrc, bo, 0,
+                    QW_CPOL_COHERENT);
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(u32x4, floatx4{y[4], y[5], y[6], y[7]}), part_rsrc, bo + 16,
+                    0, QW_CPOL_COHERENT);
+                continue;
+            }
+            if (pld) { /* all pieces of a split tile, summed in piece order */
+                float t[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) t[j] = 0.0f;
+                for (uint32_t pc = 0; pc < npart; pc++) {
+                    floatx4 p0, p1;
+                    if (pc == own) {
+                        p0 = floatx4{y[0], y[1], y[2], y[3]};
+                        p1 = floatx4{y[4], y[5], y[6], y[7]};
+                    } else {
+                        const uint32_t bo =
+                            (uint32_t)((pld - a.sk_part) + pc * QW_SPLIT_PART + poff) * 4;
+                        p0 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             part_rsrc, bo, 0, QW_CPOL_COHERENT));
+                        p1 = __builtin_bit_cast(floatx4,
+                                                __builtin_amdgcn_raw_buffer_load_b128(
+                                                    part_rsrc, bo + 16, 0, QW_CPOL_COHERENT));
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; j++) t[j] += p0[j], t[4 + j] += p1[j];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = t[j];
             }
 #pragma unroll
             for (int j = 0; j < 8; j++) {
@@ -362,9 +412,14 @@ __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &
     }
 }
 
-template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int FDB>
-__device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned char *lds,
-                                             unsigned char *lds_b) {
+/* Sums of tile (tm, tn) over k-steps [kb, ke) (64 k each) into acc; the
+ * PF == 1, 2 pipelines take the whole k range only. Ends with the LDS
+ * stages free (after a barrier). */
+template <int INT8, int WM, int WN, int MI, int NI, int PF, int FDB>
+__device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned char *lds,
+                                              unsigned char *lds_b, uint32_t tm, uint32_t tn,
+                                              uint32_t kb, uint32_t ke,
+                                              floatx16 (&acc)[NI][MI]) {
     typedef GemmShape<WM, WN, MI, NI> S;
     /* wave index in a scalar register: the LDS destinations of the direct
      * loads (M0) and the fragment bases then need no per-slice
@@ -373,9 +428,6 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / WN, wn = wave % WN;
     const uint32_t h = lane >> 5, i32 = lane & 31;
-
-    uint32_t tm, tn;
-    gemm_tile(a, tm, tn);
     const uint32_t m0 = tm * S::BM, n0 = tn * S::BN;
 
     /* ---- global loads: raw buffer loads with 32-bit byte offsets (one
@@ -436,7 +488,6 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
         }
     };
 
-    floatx16 acc[NI][MI]; /* C^T blocks */
 #pragma unroll
     for (int ni = 0; ni < NI; ni++)
 #pragma unroll
@@ -450,7 +501,7 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     const uint32_t swz = (i32 >> 1) & 7u;
 #define QW_FRAG(row, ks) ((row) * 128u + (((2 * (ks) + h) ^ swz) << 4))
 
-    const uint32_t KT = a.k / GBK;
+    const uint32_t KT = ke;
 #define QW_COMPUTE_AT(base)                                                                     \
     do {                                                                                        \
         const unsigned char *As = (base);                                                       \
@@ -520,24 +571,25 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
         /* prologue: slice 0 into stage lds (A/W direct; int8 W via regs) */
         {
             typedef __attribute__((address_space(3))) void lds_void;
+            const uint32_t k0 = kb * GBK;
 #pragma unroll
             for (int j = 0; j < A_DL; j++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rsrc, (lds_void *)(lds + c.a_dst0 + j * 1024),
-                                                         16, c.a_dvoff[j], 0, 0, 0);
+                                                         16, c.a_dvoff[j] + k0 * 2, 0, 0, 0);
 #pragma unroll
             for (int j = 0; j < W_DL; j++)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    w_rsrc, (lds_void *)(lds + S::A_BYTES + c.w_dst0 + j * 1024), 16, c.w_dvoff[j], 0,
-                    0, 0);
+                    w_rsrc, (lds_void *)(lds + S::A_BYTES + c.w_dst0 + j * 1024), 16,
+                    c.w_dvoff[j] + k0 * 2, 0, 0, 0);
             if (INT8) {
-                QW_LOAD(0, 0);
+                QW_LOAD(0, k0);
                 store_lds(ra[0], rw[0], 0);
             }
         }
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): direct loads landed */
         __syncthreads();
-        for (uint32_t kt = 0; kt < KT; kt++) {
-            const uint32_t odd = kt & 1;
+        for (uint32_t kt = kb; kt < KT; kt++) {
+            const uint32_t odd = (kt - kb) & 1;
             const uint32_t nk = (kt + 1 < KT ? kt + 1 : kt) * GBK;
             gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS>(
                 c, acc, odd ? lds_b : lds, odd ? lds : lds_b, QW_K(nk));
@@ -577,7 +629,23 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
 #undef QW_COMPUTE_AT
 #undef QW_LOAD
 #undef QW_FRAG
+}
 
+/* Epilogue of a finished tile (bf16 output plus the EPI op), or with pst the
+ * fp32 sums of one piece of a split tile, or with pld the sum of all its
+ * pieces followed by the epilogue */
+template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF>
+__device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char *lds,
+                                            unsigned char *lds_b, uint32_t tm, uint32_t tn,
+                                            floatx16 (&acc)[NI][MI], float *pst = nullptr,
+                                            const float *pld = nullptr, uint32_t npart = 0,
+                                            uint32_t own = 0) {
+    typedef GemmShape<WM, WN, MI, NI> S;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave / WN, wn = wave % WN;
+    const uint32_t h = lane >> 5, i32 = lane & 31;
+    const uint32_t row0 = tm * S::BM + wm * (MI * 32), col0 = tn * S::BN + wn * (NI * 32);
 #ifndef QW_EXP_NO_EPI
     if (PF == 0 && NI == 4) {
         /* the stages are free after the loop's last barrier: the first half
@@ -585,12 +653,66 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
          * 32-row slab (16.5 KB) per wave at a time */
         constexpr int NW = WM * WN, REG = 32 * (NI * 32 + 4) * 4;
         float *region = (float *)((wave < NW / 2 ? lds : lds_b) + (wave % (NW / 2)) * REG);
-        gemm_epilogue_lds<EPI, INT8, MI, NI>(a, acc, region, m0 + wm * (MI * 32),
-                                             n0 + wn * (NI * 32), h, i32, lane);
+        /* split-tile partials: row-major 256 x 256 fp32 */
+        static_assert(S::BN == 256 && S::BM * S::BN <= QW_SPLIT_PART, "partial tile size");
+        const uint32_t poff = wm * (MI * 32) * 256 + wn * (NI * 32);
+        gemm_epilogue_lds<EPI, INT8, MI, NI>(a, acc, region, row0, col0, h, i32, lane,
+                                             pst ? pst + poff : nullptr, pld ? pld + poff : nullptr,
+                                             npart, own);
         return;
     }
 #endif
-    gemm_epilogue<EPI, INT8, MI, NI>(a, acc, m0 + wm * (MI * 32), n0 + wn * (NI * 32), h, i32);
+    gemm_epilogue<EPI, INT8, MI, NI>(a, acc, row0, col0, h, i32);
+}
+
+template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int FDB>
+__device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned char *lds,
+                                             unsigned char *lds_b) {
+    const uint32_t KT = a.k / GBK;
+    const uint32_t nt = a.tiles_m * a.tiles_n;
+    const bool split = PF == 0 && NI == 4 && a.split > 1;
+    const uint32_t ndp = split ? a.dp_tiles : nt;
+    floatx16 acc[NI][MI]; /* C^T blocks */
+    uint32_t pid = blockIdx.x, tm, tn;
+    if (pid < ndp) { /* whole tile; ids XCD-remapped over the whole-tile range */
+        if ((ndp & 7u) == 0) pid = (pid & 7u) * (ndp >> 3) + (pid >> 3);
+        gemm_tile_at(a, pid, tm, tn);
+        gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB>(a, lds, lds_b, tm, tn, 0, KT, acc);
+        gemm_finish<EPI, INT8, WM, WN, MI, NI, PF>(a, lds, lds_b, tm, tn, acc);
+        return;
+    }
+    /* Piece of a split tile. Pieces are numbered k-range-major, so the
+     * workgroups resident together multiply neighbouring tiles over the same
+     * k-range and share their A and W panels in L2, as whole tiles do. */
+    __shared__ uint32_t ticket;
+    const uint32_t R = nt - ndp, S = a.split, np = R * S;
+    uint32_t q = pid - ndp;
+    if ((np & 7u) == 0) q = (q & 7u) * (np >> 3) + (q >> 3);
+    const uint32_t piece = q / R, r = q % R;
+    const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
+    gemm_tile_at(a, ndp + r, tm, tn);
+    gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB>(a, lds, lds_b, tm, tn, kb, ke, acc);
+    float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
+    gemm_finish<EPI, INT8, WM, WN, MI, NI, PF>(a, lds, lds_b, tm, tn, acc,
+                                               slots + (size_t)piece * QW_SPLIT_PART);
+    /* publish the partial (its coherent stores complete before the
+     * workgroup's barrier), then count it. Agent-scope release/acquire
+     * fences are not used: on this part they write back and invalidate the
+     * whole L2, which the other tiles' panels live in. */
+    __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the partial's stores are done */
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        ticket = __hip_atomic_fetch_add(a.sk_flag + r, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (ticket != S - 1) return;
+    /* last piece in: the others' partials are read with coherent loads */
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    gemm_finish<EPI, INT8, WM, WN, MI, NI, PF>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S,
+                                               piece);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.sk_flag + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 /* LDS of the direct-to-LDS pipeline: two stages, each also large enough

@@ -29,6 +29,15 @@ typedef struct {
     uint32_t gate_row_stride; /* elements between modulation rows */
     uint32_t tiles_m, tiles_n;
     uint32_t a_bytes, w_bytes; /* buffer-resource extents (< 2^31) */
+    /* Split tiles (split > 1): the first dp_tiles tiles (whole waves of
+     * workgroups) run one per workgroup; each remaining tile r is cut into
+     * `split` k-ranges, one workgroup each, numbered k-range-major. Every
+     * piece stores its fp32 sums in sk_part[r * split + piece]; the last to
+     * count itself in sk_flag[r] (0 between launches) adds them in piece
+     * order and runs the epilogue. split <= 1: one workgroup per tile. */
+    uint32_t dp_tiles, split;
+    float *sk_part;
+    uint32_t *sk_flag;
 } qw_gemm_args;
 
 typedef struct {

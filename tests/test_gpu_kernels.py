@@ -50,6 +50,18 @@ def test_quantize_and_dequant_bit_exact(gpu, qd, oracle, rows, cols):
     assert np.array_equal(dq.read(), deq_ref)
 
 
+def bf16_neighbours(v):
+    """The two bf16 values next to each element of v (bit patterns), by
+    magnitude one step down and one step up; around zero, +-the smallest
+    subnormal."""
+    v = v.astype(np.uint16)
+    mag = v & np.uint16(0x7FFF)
+    zero = mag == 0
+    down = np.where(zero, np.uint16(0x0001), v - np.uint16(1)).astype(np.uint16)
+    up = np.where(zero, np.uint16(0x8001), v + np.uint16(1)).astype(np.uint16)
+    return down, up
+
+
 def assert_linear_close(oracle, got, ref, mag):
     """Two fp32 sums of the same bf16 products in different orders round
     to bf16 at most one ulp apart, except where cancellation leaves a
@@ -140,6 +152,78 @@ def test_linear_gelu_and_gate_epilogues(gpu, qd, oracle, int8, rows):
         # <= 1.13) or the gate (|g| <= 1) plus one output rounding
         ok = (d <= 2) | (diff <= 2.0 ** -13 * mag)
         assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
+
+
+# (rows, k, n, int8, epilogue). On the 256-CU part a grid of 256 x 256
+# tiles that leaves the last wave of workgroups partly filled has those tiles
+# cut into k-ranges of at least 2048, one workgroup each; the last piece of a
+# tile to finish adds the fp32 partials in piece order. 16 tiles with
+# k = 4096 are cut in 2; 10 ragged tiles (300 rows, 1032 columns) with
+# k = 8192 in 4; 12 tiles with k = 12288 (the MLP down projection's depth)
+# in 6.
+SPLIT_CASES = [
+    (512, 4096, 2048, False, "store"),
+    (300, 8192, 1032, True, "gelu"),
+    (512, 4096, 2048, False, "gate"),
+    (256, 12288, 3072, False, "store"),
+]
+
+
+@pytest.mark.parametrize("rows,k,n,int8,epi", SPLIT_CASES)
+def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
+    x = synth(oracle, rows * k, 11)
+    w = synth(oracle, n * k, 12, 0.02)
+    b = synth(oracle, n, 13, 0.02)
+    xt, bt = gpu.put(x), gpu.put(b)
+    if int8:
+        q, s = oracle.quantize_int8_rows(w, n, k)
+        wt, st = gpu.put(q), gpu.put(s)
+        lin = oracle.linear_i8(x, q, s, b, rows, k, n)
+    else:
+        wt, st = gpu.put(w), None
+        lin = oracle.linear(x, w, b, rows, k, n)
+    absx, absw = x & np.uint16(0x7FFF), w & np.uint16(0x7FFF)
+    mag = oracle.bf16_to_f32(oracle.linear(absx, absw, None, rows, k, n)).ravel()
+    outs = []
+    for rep in range(2):  # piece counters must be back at 0 for the second call
+        if epi == "gate":
+            slots = 6
+            mod = synth(oracle, 2 * slots * n, 14, 0.5)
+            rm = (np.arange(rows) % 3 == 1).astype(np.uint32)
+            h0 = synth(oracle, rows * n, 15)
+            out = gpu.put(h0)
+            gpu.linear(out, xt, wt, rows, k, n, bias=bt, wscale=st, epilogue=qd.LINEAR_GATE,
+                       modulation=gpu.put(mod), row_map=gpu.put(rm), slots=slots, gate_slot=2)
+        else:
+            out = gpu.new(rows * n, qd.BF16)
+            gpu.linear(out, xt, wt, rows, k, n, bias=bt, wscale=st,
+                       epilogue=qd.LINEAR_GELU if epi == "gelu" else qd.LINEAR_STORE)
+        gpu.submit()
+        outs.append(out.read())
+    assert np.array_equal(outs[0], outs[1]), "split-tile result differs between two calls"
+    got = outs[0]
+    if epi == "store":
+        assert_linear_close(oracle, got, lin.ravel(), mag)
+        return
+    if epi == "gate":
+        # out = bf16(h + bf16(y) g): where h and y g nearly cancel, the one
+        # flip of bf16(y) that a different summation order may cause moves
+        # the output by many of its ulps, so accept the gate of y or of
+        # either bf16 neighbour of y (each within one output ulp)
+        best = None
+        for yv in (lin.ravel(),) + bf16_neighbours(lin.ravel()):
+            want = np.empty(rows * n, np.uint16)
+            oracle.lib().qo_gate(want, h0, np.ascontiguousarray(yv), mod, rm, rows, n, slots, 2)
+            d = ulp_diff(got, want)
+            best = d if best is None else np.minimum(best, d)
+        assert best.max() <= 1, best.max()
+        return
+    want = np.empty_like(lin)
+    oracle.lib().qo_gelu_tanh(want.ravel(), lin.ravel(), lin.size)
+    d = ulp_diff(got, want.ravel())
+    diff = np.abs(oracle.bf16_to_f32(got).astype(np.float64) - oracle.bf16_to_f32(want.ravel()))
+    ok = (d <= 2) | (diff <= 2.0 ** -13 * mag)
+    assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
 def test_linear_strided_views(gpu, qd, oracle):
