@@ -60,10 +60,22 @@ void qw_dit_config_reference(qw_dit_config *cfg);
  * bias, full text prefix, 32 layers. */
 void qw_dit_config_baseline(qw_dit_config *cfg);
 
-/* reference qwen_dit.h:31-32. Loading released checkpoint shards is not
- * part of this build: returns NULL with an explanatory error. */
+/* reference qwen_dit.h:31-32 (qwen_dit.m:235-371): the reference geometry
+ * (qw_dit_config_reference with `layers` blocks) from the safetensors
+ * shards in <model_dir>/transformer, tensors by their diffusers names
+ * (img_in, txt_in.*, time_text_embed.timestep_embedder.linear_{1,2},
+ * modulation.1, norm_out.linear, proj_out, transformer_blocks.N.attn.to_{q,k,v},
+ * .to_out.0, .norm_{q,k}, .img_mlp.{gate_layer,proj,out}), bf16 with exact
+ * shapes. q, k, v rows are fused into one [3H, H] weight and gate, proj into
+ * [2F, H]. Returns NULL with the reason (missing tensor, dtype, shape, I/O). */
 qw_dit *qw_dit_create(h3_gpu *gpu, const char *model_dir, int layers,
                       char *error, size_t error_size);
+/* The same loader for any geometry of that architecture (cfg->mlp_act =
+ * SwiGLU, no shift, no biases): shapes follow cfg, and cfg->int8_weights
+ * quantises the block linears on device after loading. No counterpart in
+ * the reference. */
+qw_dit *qw_dit_load(h3_gpu *gpu, const char *model_dir,
+                    const qw_dit_config *cfg, char *error, size_t error_size);
 /* Seeded random weights, N(0, 0.02) bf16 from the counter-based generator
  * (weight stream ids below); norm_q/norm_k = 1 + N(0, 0.02); block
  * linears quantised on device when cfg->int8_weights. */

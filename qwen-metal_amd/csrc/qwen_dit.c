@@ -24,6 +24,7 @@
 #include <strings.h>
 
 #include "../../include/qwen_gpu_ext.h"
+#include "../../include/h3_weights.h"
 
 typedef struct {
     h3_gpu_tensor *w;      /* bf16 or int8 [n, k] */
@@ -110,17 +111,6 @@ void qw_dit_config_baseline(qw_dit_config *c) {
     c->int8_weights = 0;
 }
 
-qw_dit *qw_dit_create(h3_gpu *gpu, const char *model_dir, int layers, char *error,
-                      size_t error_size) {
-    (void)gpu;
-    (void)layers;
-    set_error(error, error_size,
-              "qw_dit_create(%s): loading released checkpoint shards is not part of this "
-              "build; use qw_dit_create_random",
-              model_dir ? model_dir : "(null)");
-    return NULL;
-}
-
 const qw_dit_config *qw_dit_get_config(const qw_dit *d) { return d ? &d->cfg : NULL; }
 
 /* ---------------------------------------------------------------------- */
@@ -181,6 +171,23 @@ static int check_config(const qw_dit_config *c, char *error, size_t n) {
     return 1;
 }
 
+/* conditioning buffers (2 modulation rows) */
+static int cond_buffers(qw_dit *d) {
+    h3_gpu *gpu = d->gpu;
+    const uint32_t H = d->cfg.hidden;
+    const uint32_t nmod = slots_of(&d->cfg) * H, nout = (d->cfg.adaln_shift ? 2 : 1) * H;
+    d->feat = h3_gpu_tensor_new_f32(gpu, 2 * 256);
+    d->feat_bf16 = h3_gpu_tensor_new_bf16(gpu, 2 * 256);
+    d->c_wide = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)H);
+    d->c_silu = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)H);
+    d->temb = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)H);
+    d->mod_raw = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)nmod);
+    d->modulation = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)nmod);
+    d->norm_out_mod = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)nout);
+    return d->feat && d->feat_bf16 && d->c_wide && d->c_silu && d->temb && d->mod_raw &&
+           d->modulation && d->norm_out_mod;
+}
+
 qw_dit *qw_dit_create_random(h3_gpu *gpu, const qw_dit_config *cfg, uint64_t seed,
                              char *error, size_t error_size) {
     if (!gpu) {
@@ -237,20 +244,7 @@ qw_dit *qw_dit_create_random(h3_gpu *gpu, const qw_dit_config *cfg, uint64_t see
              qw_gpu_fill_normal_bf16(gpu, L->norm_k, 0, 128, seed, QW_LAYER_STREAM(l, QW_L_NORM_K),
                                      0.02f, 1.0f);
     }
-    /* conditioning buffers (2 modulation rows) */
-    if (ok) {
-        d->feat = h3_gpu_tensor_new_f32(gpu, 2 * 256);
-        d->feat_bf16 = h3_gpu_tensor_new_bf16(gpu, 2 * 256);
-        d->c_wide = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)H);
-        d->c_silu = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)H);
-        d->temb = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)H);
-        d->mod_raw = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)nmod);
-        d->modulation = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)nmod);
-        d->norm_out_mod = h3_gpu_tensor_new_bf16(gpu, 2 * (size_t)nout);
-        ok = d->feat && d->feat_bf16 && d->c_wide && d->c_silu && d->temb && d->mod_raw &&
-             d->modulation && d->norm_out_mod;
-    }
-    ok = ok && h3_gpu_submit(gpu);
+    ok = ok && cond_buffers(d) && h3_gpu_submit(gpu);
     h3_gpu_tensor_free(tmp);
     if (!ok) {
         set_error(error, error_size, "qw_dit_create_random failed: %s", h3_gpu_error(gpu));
@@ -258,6 +252,150 @@ qw_dit *qw_dit_create_random(h3_gpu *gpu, const qw_dit_config *cfg, uint64_t see
         return NULL;
     }
     return d;
+}
+
+/* ---------------------------------------------------------------------- */
+/* checkpoint loading (qwen_dit.m:235-371)                                */
+
+/* A linear whose weight is the row-wise concatenation of named [rows_i, k]
+ * bf16 tensors; int8 => read into the temporary bf16 tensor and quantised
+ * on device (the same path as the seeded weights). */
+static int lin_load(qw_dit *d, h3_weight_store *st, qw_lin *l, uint32_t k, const char *const *names,
+                    const uint32_t *rows, int parts, int int8, h3_gpu_tensor *tmp, char *error,
+                    size_t error_size) {
+    h3_gpu *g = d->gpu;
+    uint32_t n = 0;
+    for (int i = 0; i < parts; i++) n += rows[i];
+    l->n = n;
+    l->k = k;
+    const size_t count = (size_t)n * k;
+    h3_gpu_tensor *dst = int8 ? h3_gpu_tensor_view(tmp, 0, count) : h3_gpu_tensor_new_bf16(g, count);
+    if (!dst) return set_error(error, error_size, "%s: allocation failed", names[0]);
+    int ok = 1;
+    size_t off = 0;
+    for (int i = 0; ok && i < parts; i++) {
+        const uint64_t shape[2] = {rows[i], k};
+        ok = h3_weight_read_bf16_into(st, names[i], 2, shape, dst, off, error, error_size);
+        off += (size_t)rows[i] * k;
+    }
+    if (ok && int8) {
+        l->w = h3_gpu_tensor_new_i8(g, count);
+        l->scales = h3_gpu_tensor_new_f32(g, n);
+        ok = l->w && l->scales && h3_gpu_quantize_weight_int8(g, l->w, l->scales, dst, n, k);
+        if (!ok) set_error(error, error_size, "%s: int8 quantisation failed: %s", names[0],
+                           h3_gpu_error(g));
+        h3_gpu_tensor_free(dst);
+    } else if (ok) {
+        l->w = dst;
+    } else {
+        h3_gpu_tensor_free(dst);
+    }
+    return ok;
+}
+
+static int lin_load1(qw_dit *d, h3_weight_store *st, qw_lin *l, const char *name, uint32_t n,
+                     uint32_t k, char *error, size_t error_size) {
+    const char *names[1] = {name};
+    const uint32_t rows[1] = {n};
+    return lin_load(d, st, l, k, names, rows, 1, 0, NULL, error, error_size);
+}
+
+static h3_gpu_tensor *vec_load(h3_weight_store *st, h3_gpu *g, const char *name, uint32_t n,
+                               char *error, size_t error_size) {
+    const uint64_t shape[1] = {n};
+    return h3_weight_load_bf16(st, g, name, 1, shape, error, error_size);
+}
+
+qw_dit *qw_dit_load(h3_gpu *gpu, const char *model_dir, const qw_dit_config *cfg, char *error,
+                    size_t error_size) {
+    if (!gpu || !model_dir) {
+        set_error(error, error_size, "qw_dit_load: missing gpu or model directory");
+        return NULL;
+    }
+    if (!check_config(cfg, error, error_size)) return NULL;
+    if (cfg->mlp_act != QW_MLP_SWIGLU || cfg->adaln_shift || cfg->has_bias) {
+        set_error(error, error_size,
+                  "qw_dit_load: checkpoints use the reference architecture (SwiGLU MLP, "
+                  "scale/gate modulation, no biases)");
+        return NULL;
+    }
+    char dir[4096];
+    snprintf(dir, sizeof(dir), "%s/transformer", model_dir);
+    h3_weight_store *st = h3_weight_store_open(dir, error, error_size);
+    if (!st) return NULL;
+    qw_dit *d = calloc(1, sizeof(*d));
+    if (!d) {
+        h3_weight_store_free(st);
+        set_error(error, error_size, "out of memory");
+        return NULL;
+    }
+    d->gpu = gpu;
+    d->cfg = *cfg;
+    d->profile = env_on("QWEN_BLOCK_PROFILE");
+    const uint32_t H = cfg->hidden, F = cfg->mlp_width, T = cfg->text_dim, Z = cfg->z_dim;
+    const int q8 = cfg->int8_weights;
+    h3_gpu_tensor *tmp = q8 ? h3_gpu_tensor_new_bf16(gpu, (size_t)2 * F * H > (size_t)3 * H * H
+                                                              ? (size_t)2 * F * H
+                                                              : (size_t)3 * H * H)
+                            : NULL;
+    d->layer = calloc(cfg->layers, sizeof(qw_layer));
+    int ok = d->layer && (!q8 || tmp);
+    if (!ok) set_error(error, error_size, "out of memory");
+    ok = ok && lin_load1(d, st, &d->img_in, "img_in.weight", H, Z, error, error_size);
+    ok = ok && (d->txt_norm = vec_load(st, gpu, "txt_in.text_norm.weight", T, error, error_size));
+    ok = ok && lin_load1(d, st, &d->txt_in1, "txt_in.in_layer.weight", H, T, error, error_size);
+    ok = ok && lin_load1(d, st, &d->txt_in2, "txt_in.out_layer.weight", H, H, error, error_size);
+    ok = ok && lin_load1(d, st, &d->time_l1, "time_text_embed.timestep_embedder.linear_1.weight",
+                         H, 256, error, error_size);
+    ok = ok && lin_load1(d, st, &d->time_l2, "time_text_embed.timestep_embedder.linear_2.weight",
+                         H, H, error, error_size);
+    ok = ok && lin_load1(d, st, &d->mod, "modulation.1.weight", 4 * H, H, error, error_size);
+    ok = ok && lin_load1(d, st, &d->norm_out, "norm_out.linear.weight", H, H, error, error_size);
+    ok = ok && lin_load1(d, st, &d->proj_out, "proj_out.weight", Z, H, error, error_size);
+    for (uint32_t l = 0; ok && l < cfg->layers; l++) {
+        qw_layer *L = &d->layer[l];
+        char q[160], k[160], v[160], o[160], nq[160], nk[160], gt[160], pj[160], ot[160];
+        snprintf(q, sizeof(q), "transformer_blocks.%u.attn.to_q.weight", l);
+        snprintf(k, sizeof(k), "transformer_blocks.%u.attn.to_k.weight", l);
+        snprintf(v, sizeof(v), "transformer_blocks.%u.attn.to_v.weight", l);
+        snprintf(o, sizeof(o), "transformer_blocks.%u.attn.to_out.0.weight", l);
+        snprintf(nq, sizeof(nq), "transformer_blocks.%u.attn.norm_q.weight", l);
+        snprintf(nk, sizeof(nk), "transformer_blocks.%u.attn.norm_k.weight", l);
+        snprintf(gt, sizeof(gt), "transformer_blocks.%u.img_mlp.gate_layer.weight", l);
+        snprintf(pj, sizeof(pj), "transformer_blocks.%u.img_mlp.proj.weight", l);
+        snprintf(ot, sizeof(ot), "transformer_blocks.%u.img_mlp.out.weight", l);
+        /* fused [q; k; v] and [gate; proj] rows, as the kernels take them */
+        const char *qkv[3] = {q, k, v}, *fc1[2] = {gt, pj}, *out[1] = {o}, *fc2[1] = {ot};
+        const uint32_t rq[3] = {H, H, H}, rf[2] = {F, F}, rh[1] = {H};
+        ok = lin_load(d, st, &L->qkv, H, qkv, rq, 3, q8, tmp, error, error_size) &&
+             lin_load(d, st, &L->out, H, out, rh, 1, q8, tmp, error, error_size) &&
+             lin_load(d, st, &L->fc1, H, fc1, rf, 2, q8, tmp, error, error_size) &&
+             lin_load(d, st, &L->fc2, F, fc2, rh, 1, q8, tmp, error, error_size) &&
+             (L->norm_q = vec_load(st, gpu, nq, 128, error, error_size)) &&
+             (L->norm_k = vec_load(st, gpu, nk, 128, error, error_size));
+    }
+    if (ok && !cond_buffers(d)) ok = set_error(error, error_size, "out of memory");
+    if (ok && !h3_gpu_submit(gpu))
+        ok = set_error(error, error_size, "qw_dit_load: %s", h3_gpu_error(gpu));
+    h3_gpu_tensor_free(tmp);
+    h3_weight_store_free(st);
+    if (!ok) {
+        qw_dit_free(d);
+        return NULL;
+    }
+    return d;
+}
+
+qw_dit *qw_dit_create(h3_gpu *gpu, const char *model_dir, int layers, char *error,
+                      size_t error_size) {
+    qw_dit_config cfg;
+    qw_dit_config_reference(&cfg);
+    if (layers <= 0 || layers > 256) {
+        set_error(error, error_size, "qw_dit_create: layers %d out of range", layers);
+        return NULL;
+    }
+    cfg.layers = (uint32_t)layers;
+    return qw_dit_load(gpu, model_dir, &cfg, error, error_size);
 }
 
 void qw_dit_free(qw_dit *d) {

@@ -33,6 +33,19 @@ class Stats(C.Structure):
         ("gpu_seconds", C.c_double)]
 
 
+class StTensor(C.Structure):
+    """h3_st_tensor (include/h3_safetensors.h)"""
+    _fields_ = [("name", C.c_char_p), ("dtype", C.c_int), ("ndim", C.c_int),
+                ("shape", C.c_uint64 * 8), ("data_begin", C.c_uint64),
+                ("data_end", C.c_uint64), ("file_offset", C.c_uint64)]
+
+
+class StHeader(C.Structure):
+    """h3_st_header (include/h3_safetensors.h)"""
+    _fields_ = [("path", C.c_char_p), ("file_size", C.c_uint64), ("header_size", C.c_uint64),
+                ("tensors", C.POINTER(StTensor)), ("tensor_count", C.c_size_t)]
+
+
 class DitConfig(C.Structure):
     _fields_ = [("hidden", u32), ("heads", u32), ("mlp_width", u32), ("text_dim", u32),
                 ("z_dim", u32), ("layers", u32), ("mlp_act", C.c_int),
@@ -164,6 +177,22 @@ SIGNATURES = {
     "qw_pipe_schedule": (C.c_int, [u32, u32, vp, u32, vp, vp, C.c_char_p, sz]),
     "qw_pipe_rope_tables": (C.c_int, [vp, u32, u32, u32, vp, vp, C.c_char_p, sz]),
     "qw_pipe_rope_tables_host": (None, [u32, u32, u32, vp, vp]),
+    "h3_st_read_header": (C.c_int, [C.c_char_p, vp, C.c_char_p, sz]),
+    "h3_st_free_header": (None, [vp]),
+    "h3_st_find": (vp, [vp, C.c_char_p]),
+    "h3_st_tensor_elements": (C.c_uint64, [vp]),
+    "h3_st_read_data": (C.c_int, [vp, vp, vp, sz, C.c_char_p, sz]),
+    "h3_dtype_size": (sz, [C.c_int]),
+    "h3_dtype_name": (C.c_char_p, [C.c_int]),
+    "h3_weight_store_open": (vp, [C.c_char_p, C.c_char_p, sz]),
+    "h3_weight_store_free": (None, [vp]),
+    "h3_weight_store_shards": (sz, [vp]),
+    "h3_weight_find": (vp, [vp, C.c_char_p, vp]),
+    "h3_weight_load_bf16": (vp, [vp, vp, C.c_char_p, C.c_int, vp, C.c_char_p, sz]),
+    "h3_weight_load_f32": (vp, [vp, vp, C.c_char_p, C.c_int, vp, C.c_char_p, sz]),
+    "h3_weight_read_bf16_into": (C.c_int, [vp, C.c_char_p, C.c_int, vp, vp, sz, C.c_char_p,
+                                           sz]),
+    "qw_dit_load": (vp, [vp, C.c_char_p, C.POINTER(DitConfig), C.c_char_p, sz]),
     "qw_pipe_denoise": (C.c_int, [vp, vp, vp, u32, vp, u32, vp, u32, u32, u32, C.c_float, vp,
                                   u32, vp, C.c_char_p, sz]),
 }
@@ -312,13 +341,20 @@ class Gpu:
 
 
 class Dit:
-    def __init__(self, gpu, cfg: dict, seed: int):
+    def __init__(self, gpu, cfg: dict, seed: int = 0, model_dir=None):
+        """Seeded random weights (qw_dit_create_random), or with model_dir
+        the safetensors checkpoint under model_dir/transformer (qw_dit_load)."""
         self.gpu = gpu
         c = DitConfig(**cfg)
         err = C.create_string_buffer(1024)
-        self.h = lib().qw_dit_create_random(gpu.h, C.byref(c), seed, err, 1024)
-        if not self.h:
-            raise RuntimeError("qw_dit_create_random: " + err.value.decode())
+        if model_dir is not None:
+            self.h = lib().qw_dit_load(gpu.h, str(model_dir).encode(), C.byref(c), err, 1024)
+            if not self.h:
+                raise RuntimeError("qw_dit_load: " + err.value.decode())
+        else:
+            self.h = lib().qw_dit_create_random(gpu.h, C.byref(c), seed, err, 1024)
+            if not self.h:
+                raise RuntimeError("qw_dit_create_random: " + err.value.decode())
         self.cfg = lib().qw_dit_get_config(self.h).contents
 
     def forward_batch(self, text_in, text_rows, latents, image_rows, batch, sigma, rope_cos,

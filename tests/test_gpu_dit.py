@@ -180,6 +180,119 @@ def test_denoise_loop(gpu, qd, oracle, case, monkeypatch):
     assert rel_l2(runs[0] - x0, x - x0) < 2e-2
 
 
+def _weight_streams():
+    """The generator stream ids of qw_dit_create_random, from include/qwen_dit.h."""
+    import os
+    import re
+    from conftest import ROOT
+    text = open(os.path.join(ROOT, "include", "qwen_dit.h")).read()
+    ids = {}
+    for body in re.findall(r"enum\s*\{([^}]*)\}", text):
+        if "QW_W_IMG_IN" not in body and "QW_L_QKV" not in body:
+            continue
+        nxt = 0
+        for item in body.replace("\n", " ").split(","):
+            item = item.strip()
+            if not item:
+                continue
+            name, _, val = item.partition("=")
+            nxt = int(val) if val.strip() else nxt
+            ids[name.strip()] = nxt
+            nxt += 1
+    return ids
+
+
+def _write_checkpoint(oracle, c, seed, root, drop=None, reshape=None):
+    """The weights qw_dit_create_random(c, seed) generates, as a two-shard
+    checkpoint under root/transformer with the reference's tensor names
+    (qwen_dit.m:263-344): fused qkv rows split into to_q/k/v, fc1 rows into
+    gate_layer/proj."""
+    torch = pytest.importorskip("torch")
+    st = pytest.importorskip("safetensors.torch")
+    ids = _weight_streams()
+    H, F, T, Z = c["hidden"], c["mlp_width"], c["text_dim"], c["z_dim"]
+
+    def w(n, stream, std=0.02, off=0.0):
+        return oracle.fill_normal_bf16(n, seed, stream, std, off)
+
+    def layer(l, f):
+        return 256 * (l + 1) + ids[f]
+
+    t = {"img_in.weight": (w(H * Z, ids["QW_W_IMG_IN"]), (H, Z)),
+         "txt_in.text_norm.weight": (w(T, ids["QW_W_TXT_NORM"]), (T,)),
+         "txt_in.in_layer.weight": (w(H * T, ids["QW_W_TXT_IN1"]), (H, T)),
+         "txt_in.out_layer.weight": (w(H * H, ids["QW_W_TXT_IN2"]), (H, H)),
+         "time_text_embed.timestep_embedder.linear_1.weight": (w(H * 256, ids["QW_W_TIME_L1"]),
+                                                               (H, 256)),
+         "time_text_embed.timestep_embedder.linear_2.weight": (w(H * H, ids["QW_W_TIME_L2"]),
+                                                               (H, H)),
+         "modulation.1.weight": (w(4 * H * H, ids["QW_W_MOD"]), (4 * H, H)),
+         "norm_out.linear.weight": (w(H * H, ids["QW_W_NORM_OUT"]), (H, H)),
+         "proj_out.weight": (w(Z * H, ids["QW_W_PROJ_OUT"]), (Z, H))}
+    for l in range(c["layers"]):
+        p = f"transformer_blocks.{l}."
+        qkv = w(3 * H * H, layer(l, "QW_L_QKV"))
+        fc1 = w(2 * F * H, layer(l, "QW_L_FC1"))
+        t[p + "attn.to_q.weight"] = (qkv[:H * H], (H, H))
+        t[p + "attn.to_k.weight"] = (qkv[H * H:2 * H * H], (H, H))
+        t[p + "attn.to_v.weight"] = (qkv[2 * H * H:], (H, H))
+        t[p + "attn.to_out.0.weight"] = (w(H * H, layer(l, "QW_L_OUT")), (H, H))
+        t[p + "attn.norm_q.weight"] = (w(128, layer(l, "QW_L_NORM_Q"), off=1.0), (128,))
+        t[p + "attn.norm_k.weight"] = (w(128, layer(l, "QW_L_NORM_K"), off=1.0), (128,))
+        t[p + "img_mlp.gate_layer.weight"] = (fc1[:F * H], (F, H))
+        t[p + "img_mlp.proj.weight"] = (fc1[F * H:], (F, H))
+        t[p + "img_mlp.out.weight"] = (w(H * F, layer(l, "QW_L_FC2")), (H, F))
+    if drop:
+        del t[drop]
+    if reshape:
+        arr, shp = t[reshape]
+        t[reshape] = (arr, (shp[-1], shp[0]) if len(shp) == 2 else shp)
+    d = root / "transformer"
+    d.mkdir(parents=True, exist_ok=True)
+    names = sorted(t)
+    for i, part in enumerate((names[::2], names[1::2])):
+        st.save_file({n: torch.from_numpy(t[n][0].astype(np.int16)).view(torch.bfloat16)
+                      .reshape(t[n][1]) for n in part},
+                     str(d / f"diffusion_pytorch_model-{i + 1:05d}-of-00002.safetensors"))
+    return root
+
+
+@pytest.mark.parametrize("int8", [0, 1])
+def test_checkpoint_loader_matches_seeded_model(gpu, qd, oracle, tmp_path, int8):
+    """qw_dit_load / qw_dit_create (qwen_dit.m:235-371) on a checkpoint that
+    holds exactly the seeded weights: the forward (batch 2, 16 text + 8x8
+    image rows) is bit-identical to the seeded model's, with bf16 weights
+    and with the block linears quantised to int8 after loading."""
+    c = cfg("small", int8_weights=int8, **REF_VARIANT)
+    root = _write_checkpoint(oracle, c, 21, tmp_path)
+    text, lat, cos, sin = _inputs(oracle, c, 2, 16, 8, 8, 4)
+    ins = [gpu.put(text), gpu.put(lat), gpu.put(cos), gpu.put(sin)]
+    outs = []
+    for dit in (qd.Dit(gpu, c, 21), qd.Dit(gpu, c, model_dir=root)):
+        out = gpu.new(2 * 80 * c["z_dim"], qd.BF16)
+        dit.forward_batch(ins[0], 16, ins[1], 64, 2, 0.4, ins[2], ins[3], out)
+        gpu.submit()
+        outs.append(out.read())
+        dit.close()
+    assert np.array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("fault", ["missing", "shape"])
+def test_checkpoint_loader_errors(gpu, qd, oracle, tmp_path, fault):
+    """A missing tensor or a transposed one fails with its name; the
+    reference geometry entry point refuses a checkpoint of another geometry."""
+    import ctypes as C
+    c = cfg("small", **REF_VARIANT)
+    name = "transformer_blocks.1.img_mlp.out.weight"
+    root = _write_checkpoint(oracle, c, 5, tmp_path, drop=name if fault == "missing" else None,
+                             reshape=name if fault == "shape" else None)
+    with pytest.raises(RuntimeError, match=name.replace(".", r"\.")):
+        qd.Dit(gpu, c, model_dir=root)
+    err = C.create_string_buffer(512)
+    assert not qd.lib().qw_dit_create(gpu.h, str(root).encode(), 3, err, 512)
+    assert b"shape" in err.value or b"missing" in err.value
+
+
 def test_forward_no_text_rows(gpu, qd, oracle):
     """dit_fixture case a topology: image rows only."""
     c = cfg("small", **REF_VARIANT)
