@@ -240,6 +240,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-breakdown", action="store_true")
+    ap.add_argument("--no-denoise", action="store_true",
+                    help="skip the 8-step 512x512 denoise-loop measurement")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="only launch a calibration copy and the dominant GEMM (for --pmc)")
     args = ap.parse_args()
@@ -299,7 +301,7 @@ def main():
                     "kernel": "qw_gemm_bf16_gelu_w8 (up-projection, M=8704 K=3072 N=12288, "
                               "int8 weight widened by qw_widen_i8_bf16, scale in the epilogue)",
                     "flop_per_launch": fl, "ms_per_launch": up["gemm_ms"]}
-    den = None if args.no_breakdown else denoise_512(qd, gpu)
+    den = None if args.no_breakdown or args.no_denoise else denoise_512(qd, gpu)
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": "DiT ms/step @1024^2 (4352 tok, CFG b=2); linear+SDPA TFLOP/s & % MFMA peak",
