@@ -138,6 +138,35 @@ int qw_dit_block(qw_dit *dit, int layer, h3_gpu_tensor *hidden,
                  h3_gpu_tensor *k_out, h3_gpu_tensor *v_out,
                  h3_gpu_tensor *debug_attn, char *error, size_t error_size);
 
+/* reference qwen_dit.h:133-139 (qwen_dit.m:1572-1648): text runs from the
+ * rows of text_in at src_offset, image runs from the rows of latents at
+ * src_offset, in segs order into joint. Each run is embedded straight into
+ * its joint rows (the embedding is row-wise). */
+int qw_dit_embed_segments(qw_dit *dit, const h3_gpu_tensor *text_in,
+                          const h3_gpu_tensor *latents,
+                          const qw_dit_segment *segs, uint32_t seg_count,
+                          h3_gpu_tensor *joint, char *error,
+                          size_t error_size);
+
+/* reference qwen_dit.h:166-181 (qwen_dit.m:1667-1967): ti2i forward over a
+ * segmented joint sequence whose last run is the target image. Rows before
+ * it modulate from t = 0, the target from sigma; attention is block-causal
+ * as a prefix table (qw_dit_prefix_limits). cache_slot (0 or 1) keeps the
+ * K/V of every row of every layer from a full pass; a later call with the
+ * same run layout recomputes only the target rows, against those cached
+ * K/V, and writes only the target rows of output. Output [rows, z_dim]. */
+int qw_dit_forward_ti2i(qw_dit *dit, const h3_gpu_tensor *text_in,
+                        const h3_gpu_tensor *latents,
+                        const qw_dit_segment *segs, uint32_t seg_count,
+                        uint32_t cache_slot, const h3_gpu_tensor *rope_cos,
+                        const h3_gpu_tensor *rope_sin, float sigma,
+                        h3_gpu_tensor *output, char *error,
+                        size_t error_size);
+
+/* reference qwen_dit.h:35-40: drop both ti2i caches (they hold one
+ * request's conditioning; call at the end of every ti2i generation). */
+void qw_dit_ti2i_cache_clear(qw_dit *dit);
+
 /* reference qwen_dit.h:141-145 */
 void qw_dit_prefix_limits(const qw_dit_segment *segs, uint32_t seg_count,
                           uint32_t *limits);

@@ -134,6 +134,12 @@ def lib():
                                  u16p, C.c_uint32, C.c_float, f32p, f32p,
                                  C.c_uint32, u16p]
         L.qo_num_threads.restype = C.c_int
+        L.qo_forward_ti2i.restype = C.c_int
+        L.qo_forward_ti2i.argtypes = [C.POINTER(QoModel), C.c_void_p, C.c_uint32, C.c_void_p,
+                                      C.c_uint32, C.c_void_p, C.c_uint32, C.c_float, f32p,
+                                      f32p, C.c_uint32, u16p]
+        L.qo_prefix_limits.restype = None
+        L.qo_prefix_limits.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p]
         _LIB = L
     return _LIB
 
@@ -215,6 +221,22 @@ def timestep_features(sigmas):
     return out
 
 
+class Segment(C.Structure):
+    """qo_segment / qw_dit_segment: rows, is_image, src_offset"""
+    _fields_ = [("rows", C.c_uint32), ("is_image", C.c_int), ("src_offset", C.c_uint32)]
+
+
+def segment_array(segs):
+    return (Segment * len(segs))(*[Segment(r, int(i), o) for r, i, o in segs])
+
+
+def prefix_limits(segs):
+    rows = sum(r for r, _, _ in segs)
+    out = np.empty(rows, np.uint32)
+    lib().qo_prefix_limits(segment_array(segs), len(segs), out.ctypes.data)
+    return out
+
+
 class Model:
     """Seeded random DiT (same weight streams as the GPU library)."""
 
@@ -243,6 +265,20 @@ class Model:
                               np.ascontiguousarray(rope_sin), layers, out)
         if not ok:
             raise RuntimeError("qo_forward failed")
+        return out
+
+    def forward_ti2i(self, text_in, text_total, latents, image_total, segs, sigma,
+                     rope_cos, rope_sin, layers):
+        """segs: [(rows, is_image, src_offset), ...]; output [rows, z_dim]."""
+        seg = segment_array(segs)
+        rows = sum(r for r, _, _ in segs)
+        out = np.empty((rows, self.cfg.z_dim), np.uint16)
+        ok = lib().qo_forward_ti2i(C.byref(self.m), ptr(text_in) if text_total else None,
+                                   text_total, ptr(np.ascontiguousarray(latents)), image_total,
+                                   seg, len(segs), float(sigma), np.ascontiguousarray(rope_cos),
+                                   np.ascontiguousarray(rope_sin), layers, out)
+        if not ok:
+            raise RuntimeError("qo_forward_ti2i failed")
         return out
 
     def block(self, layer, hidden, modulation, rope_cos, rope_sin, row_map,

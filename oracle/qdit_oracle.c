@@ -986,3 +986,68 @@ int qo_forward(const qo_model *m, const uint16_t *text_in, uint32_t text_rows,
     free(nout);
     return 1;
 }
+
+void qo_prefix_limits(const qo_segment *segs, uint32_t seg_count, uint32_t *limits) {
+    /* qwen_dit.m:1651-1665 */
+    uint32_t start = 0;
+    for (uint32_t s = 0; s < seg_count; s++) {
+        for (uint32_t r = 0; r < segs[s].rows; r++)
+            limits[start + r] = segs[s].is_image ? start + segs[s].rows : start + r + 1;
+        start += segs[s].rows;
+    }
+}
+
+int qo_forward_ti2i(const qo_model *m, const uint16_t *text_in, uint32_t text_total,
+                    const uint16_t *latents, uint32_t image_total, const qo_segment *segs,
+                    uint32_t seg_count, float sigma, const float *rope_cos,
+                    const float *rope_sin, uint32_t layers, uint16_t *output) {
+    if (!seg_count || !segs[seg_count - 1].is_image || layers > m->cfg.layers) return 0;
+    uint32_t rows = 0;
+    for (uint32_t s = 0; s < seg_count; s++) {
+        const uint32_t have = segs[s].is_image ? image_total : text_total;
+        if (segs[s].src_offset > have || segs[s].rows > have - segs[s].src_offset) return 0;
+        rows += segs[s].rows;
+    }
+    const size_t H = m->cfg.hidden;
+    const uint32_t target = segs[seg_count - 1].rows, prefix = rows - target;
+    /* qwen_dit.m:1572-1648: project every source row, then scatter runs */
+    uint16_t *proj = malloc(sizeof(uint16_t) * (size_t)(text_total + image_total) * H);
+    uint16_t *joint = malloc(sizeof(uint16_t) * (size_t)rows * H);
+    uint32_t *row_map = malloc(sizeof(uint32_t) * rows);
+    uint32_t *limits = malloc(sizeof(uint32_t) * rows);
+    if (!proj || !joint || !row_map || !limits) {
+        free(proj);
+        free(joint);
+        free(row_map);
+        free(limits);
+        return 0;
+    }
+    qo_embed(m, text_in, text_total, latents, image_total, proj);
+    uint32_t at = 0;
+    for (uint32_t s = 0; s < seg_count; s++) {
+        const size_t src = (size_t)(segs[s].is_image ? text_total : 0) + segs[s].src_offset;
+        memcpy(joint + (size_t)at * H, proj + src * H, sizeof(uint16_t) * segs[s].rows * H);
+        at += segs[s].rows;
+    }
+    /* qwen_dit.m:1725-1729: only the target run reads the sampled step */
+    for (uint32_t i = 0; i < rows; i++) row_map[i] = i < prefix ? 1u : 0u;
+    qo_prefix_limits(segs, seg_count, limits);
+    float sig[2] = {sigma, 0.0f}, feat[512];
+    qo_timestep_features(sig, 2, feat);
+    const uint32_t slots = m->cfg.adaln_shift ? 6 : 4;
+    uint16_t *temb = malloc(sizeof(uint16_t) * 2 * H);
+    uint16_t *mod = malloc(sizeof(uint16_t) * 2 * slots * H);
+    uint16_t *nout = malloc(sizeof(uint16_t) * 2 * m->norm_out.n);
+    qo_conditioning(m, feat, 2, temb, mod, nout);
+    for (uint32_t l = 0; l < layers; l++)
+        qo_block(m, (int)l, joint, mod, rope_cos, rope_sin, row_map, rows, 0, limits, NULL);
+    qo_final(m, joint, nout, row_map, rows, output);
+    free(proj);
+    free(joint);
+    free(row_map);
+    free(limits);
+    free(temb);
+    free(mod);
+    free(nout);
+    return 1;
+}

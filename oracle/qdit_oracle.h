@@ -231,6 +231,27 @@ int qo_forward(const qo_model *m, const uint16_t *text_in, uint32_t text_rows,
                const float *rope_cos, const float *rope_sin, uint32_t layers,
                uint16_t *output);
 
+/* A ti2i joint-sequence run (qwen_dit.h:21-29): text rows from text_in or
+ * image rows from latents, starting at src_offset of that source. */
+typedef struct {
+    uint32_t rows;
+    int is_image;
+    uint32_t src_offset;
+} qo_segment;
+/* qwen_dit.m:1651-1665: text rows see their run up to themselves (run
+ * start + r + 1), image rows their whole run (run end); limits[rows]. */
+void qo_prefix_limits(const qo_segment *segs, uint32_t seg_count, uint32_t *limits);
+/* The ti2i forward's full pass (qwen_dit.m:1667-1860): every text_in row
+ * and every latents row projected (qwen_dit.m:1572-1648), runs scattered
+ * into the joint order, rows before the last run modulated from t = 0 and
+ * the last (target image) run from sigma, block-causal prefix limits, all
+ * blocks, the final head over every row. output [rows, z_dim]. Returns 0
+ * when the last run is not an image run or a run reads past its source. */
+int qo_forward_ti2i(const qo_model *m, const uint16_t *text_in, uint32_t text_total,
+                    const uint16_t *latents, uint32_t image_total, const qo_segment *segs,
+                    uint32_t seg_count, float sigma, const float *rope_cos,
+                    const float *rope_sin, uint32_t layers, uint16_t *output);
+
 /* Threads used by the OpenMP regions (for the baseline report). */
 int qo_num_threads(void);
 /* 0 (default): fp32 softmax probabilities; 1: probabilities rounded to

@@ -61,6 +61,14 @@ struct qw_dit {
     uint32_t rm_rows, rm_text, rm_batch;
     int profile;
     double prof_ms[P_COUNT];
+    /* ti2i cross-step caches (slot 0: guided branch, 1: CFG negative) */
+    struct qw_ti2i_cache {
+        uint32_t rows, target_rows, seg_count;
+        qw_dit_segment *segs;
+        h3_gpu_tensor **k, **v;  /* per layer [rows, H]: every row's K / V */
+        h3_gpu_tensor *th, *row0; /* target hidden [target_rows, H]; zeros */
+        int filled;
+    } ti2i[2];
 };
 
 static int set_error(char *error, size_t n, const char *fmt, ...) {
@@ -423,6 +431,7 @@ void qw_dit_free(qw_dit *d) {
                           d->temb, d->mod_raw, d->modulation, d->norm_out_mod, d->joint,
                           d->row_map};
     for (size_t i = 0; i < sizeof(t) / sizeof(t[0]); i++) h3_gpu_tensor_free(t[i]);
+    qw_dit_ti2i_cache_clear(d);
     free(d);
 }
 
@@ -627,11 +636,20 @@ int qw_dit_conditioning(qw_dit *d, const h3_gpu_tensor *features, uint32_t mod_r
 /* ---------------------------------------------------------------------- */
 /* block                                                                  */
 
+/* Attention of a block's rows against cached keys (ti2i target-only
+ * steps): the rows' own K/V are written at `base` of the [rows, H] caches,
+ * then their queries attend to all cache rows. */
+typedef struct {
+    h3_gpu_tensor *k, *v;
+    uint32_t base, rows;
+} qw_kv_cache;
+
 static int block_run(qw_dit *d, int li, h3_gpu_tensor *hidden, uint32_t batch, uint32_t rows,
                      uint32_t text_rows, const h3_gpu_tensor *modulation,
                      const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
                      const h3_gpu_tensor *row_map, const h3_gpu_tensor *kv_limit,
-                     h3_gpu_tensor *k_out, h3_gpu_tensor *v_out, h3_gpu_tensor *debug_attn) {
+                     h3_gpu_tensor *k_out, h3_gpu_tensor *v_out, h3_gpu_tensor *debug_attn,
+                     const qw_kv_cache *kvc) {
     h3_gpu *g = d->gpu;
     const qw_layer *L = &d->layer[li];
     const uint32_t H = d->cfg.hidden, F = d->cfg.mlp_width, S = slots_of(&d->cfg);
@@ -665,6 +683,19 @@ static int block_run(qw_dit *d, int li, h3_gpu_tensor *hidden, uint32_t batch, u
     ad.text_rows = text_rows;
     ad.text_causal = d->cfg.text_causal;
     ad.scale = 1.0f / sqrtf(128.0f);
+    if (kvc) { /* this step's rows into the cache, then attend to all of it */
+        ok = qw_gpu_copy_rows(g, kvc->k, (size_t)kvc->base * H, H, d->ws_qkv, H, 3 * H, M, H) &&
+             qw_gpu_copy_rows(g, kvc->v, (size_t)kvc->base * H, H, d->ws_qkv, 2 * (size_t)H,
+                              3 * H, M, H);
+        if (!ok) return 0;
+        ad.k = kvc->k;
+        ad.v = kvc->v;
+        ad.k_offset = ad.v_offset = 0;
+        ad.ldk = ad.ldv = H;
+        ad.kv_rows = kvc->rows;
+        ad.kv_limit = NULL;
+        ad.text_rows = 0; /* every query sees every cached key */
+    }
     ok = qw_gpu_attention_bf16(g, &ad);
     if (ok && k_out) ok = qw_gpu_copy_rows(g, k_out, 0, H, d->ws_qkv, H, 3 * H, M, H);
     if (ok && v_out) ok = qw_gpu_copy_rows(g, v_out, 0, H, d->ws_qkv, 2 * (size_t)H, 3 * H, M, H);
@@ -724,7 +755,7 @@ int qw_dit_block(qw_dit *d, int layer, h3_gpu_tensor *hidden, const h3_gpu_tenso
         return set_error(error, error_size, "block %d: output tensors too small", layer);
     if (!ensure_ws(d, rows)) return set_error(error, error_size, "workspace allocation failed");
     if (!block_run(d, layer, hidden, 1, rows, text_rows, modulation, rope_cos, rope_sin, row_map,
-                   kv_limit, k_out, v_out, debug_attn))
+                   kv_limit, k_out, v_out, debug_attn, NULL))
         return set_error(error, error_size, "block %d kernel failed: %s", layer,
                          h3_gpu_error(d->gpu));
     return 1;
@@ -838,7 +869,7 @@ static int forward_impl(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_r
 
     for (uint32_t l = 0; l < d->cfg.layers; l++)
         if (!block_run(d, (int)l, d->joint, batch, rows, text_rows, d->modulation, rope_cos,
-                       rope_sin, d->row_map, NULL, NULL, NULL, NULL))
+                       rope_sin, d->row_map, NULL, NULL, NULL, NULL, NULL))
             return set_error(error, error_size, "block %u kernel failed: %s", l, h3_gpu_error(g));
 
     prof_begin(d);
@@ -884,4 +915,202 @@ int qw_dit_forward(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_rows,
            (h3_gpu_submit(d->gpu) && h3_gpu_begin(d->gpu)
                 ? 1
                 : set_error(error, error_size, "forward failed: %s", h3_gpu_error(d->gpu)));
+}
+
+/* ---------------------------------------------------------------------- */
+/* ti2i: segmented joint sequence, block-causal prefix attention, and the  */
+/* cross-step K/V cache (qwen_dit.m:1572-1665, 1667-1967)                  */
+
+static int segs_valid(const qw_dit *d, const h3_gpu_tensor *text_in, const h3_gpu_tensor *latents,
+                      const qw_dit_segment *segs, uint32_t seg_count, uint32_t *rows, char *error,
+                      size_t error_size) {
+    const size_t text_total = text_in ? h3_gpu_tensor_elements(text_in) / d->cfg.text_dim : 0;
+    const size_t image_total = latents ? h3_gpu_tensor_elements(latents) / d->cfg.z_dim : 0;
+    uint64_t n = 0;
+    if (!segs || !seg_count) return set_error(error, error_size, "ti2i: no runs");
+    for (uint32_t s = 0; s < seg_count; s++) {
+        const size_t have = segs[s].is_image ? image_total : text_total;
+        if (!segs[s].rows || segs[s].src_offset > have || segs[s].rows > have - segs[s].src_offset)
+            return set_error(error, error_size, "ti2i: run %u (%u %s rows at %u) outside its source",
+                             s, segs[s].rows, segs[s].is_image ? "image" : "text",
+                             segs[s].src_offset);
+        n += segs[s].rows;
+    }
+    if (n > (1u << 24)) return set_error(error, error_size, "ti2i: %llu rows", (unsigned long long)n);
+    *rows = (uint32_t)n;
+    return 1;
+}
+
+int qw_dit_embed_segments(qw_dit *d, const h3_gpu_tensor *text_in, const h3_gpu_tensor *latents,
+                          const qw_dit_segment *segs, uint32_t seg_count, h3_gpu_tensor *joint,
+                          char *error, size_t error_size) {
+    /* qwen_dit.m:1572-1648: the embedding is row-wise, so each run is
+     * embedded straight into its joint rows (no projection of unused rows,
+     * no scatter copies) */
+    if (!d) return set_error(error, error_size, "no dit");
+    uint32_t rows;
+    if (!segs_valid(d, text_in, latents, segs, seg_count, &rows, error, error_size)) return 0;
+    const uint32_t H = d->cfg.hidden;
+    if (!joint || h3_gpu_tensor_elements(joint) < (size_t)rows * H)
+        return set_error(error, error_size, "joint tensor too small");
+    uint32_t at = 0;
+    for (uint32_t s = 0; s < seg_count; s++) {
+        const int img = segs[s].is_image;
+        const int ok =
+            img ? embed_one(d, NULL, 0, 0, latents, (size_t)segs[s].src_offset * d->cfg.z_dim,
+                            segs[s].rows, joint, (size_t)at * H)
+                : embed_one(d, text_in, (size_t)segs[s].src_offset * d->cfg.text_dim, segs[s].rows,
+                            NULL, 0, 0, joint, (size_t)at * H);
+        if (!ok) return set_error(error, error_size, "embed of run %u failed: %s", s,
+                                  h3_gpu_error(d->gpu));
+        at += segs[s].rows;
+    }
+    return 1;
+}
+
+static void cache_drop(qw_dit *d, struct qw_ti2i_cache *t) {
+    for (uint32_t l = 0; l < d->cfg.layers; l++) {
+        if (t->k) h3_gpu_tensor_free(t->k[l]);
+        if (t->v) h3_gpu_tensor_free(t->v[l]);
+    }
+    free(t->k);
+    free(t->v);
+    free(t->segs);
+    h3_gpu_tensor_free(t->th);
+    h3_gpu_tensor_free(t->row0);
+    memset(t, 0, sizeof(*t));
+}
+
+void qw_dit_ti2i_cache_clear(qw_dit *d) {
+    if (!d) return;
+    cache_drop(d, &d->ti2i[0]);
+    cache_drop(d, &d->ti2i[1]);
+}
+
+static int cache_alloc(qw_dit *d, struct qw_ti2i_cache *t, uint32_t rows, uint32_t target,
+                       const qw_dit_segment *segs, uint32_t seg_count) {
+    cache_drop(d, t);
+    const size_t n = (size_t)rows * d->cfg.hidden;
+    t->k = calloc(d->cfg.layers, sizeof(*t->k));
+    t->v = calloc(d->cfg.layers, sizeof(*t->v));
+    t->segs = malloc(sizeof(*segs) * seg_count);
+    uint32_t *zero = calloc(target, sizeof(uint32_t));
+    int ok = t->k && t->v && t->segs && zero;
+    for (uint32_t l = 0; ok && l < d->cfg.layers; l++)
+        ok = (t->k[l] = h3_gpu_tensor_new_bf16(d->gpu, n)) &&
+             (t->v[l] = h3_gpu_tensor_new_bf16(d->gpu, n));
+    ok = ok && (t->th = h3_gpu_tensor_new_bf16(d->gpu, (size_t)target * d->cfg.hidden)) &&
+         (t->row0 = h3_gpu_tensor_from_u32(d->gpu, zero, target));
+    free(zero);
+    if (!ok) {
+        cache_drop(d, t);
+        return 0;
+    }
+    memcpy(t->segs, segs, sizeof(*segs) * seg_count);
+    t->rows = rows;
+    t->target_rows = target;
+    t->seg_count = seg_count;
+    return 1;
+}
+
+int qw_dit_forward_ti2i(qw_dit *d, const h3_gpu_tensor *text_in, const h3_gpu_tensor *latents,
+                        const qw_dit_segment *segs, uint32_t seg_count, uint32_t cache_slot,
+                        const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin, float sigma,
+                        h3_gpu_tensor *output, char *error, size_t error_size) {
+    if (error && error_size) error[0] = '\0';
+    if (!d) return set_error(error, error_size, "no dit");
+    h3_gpu *g = d->gpu;
+    uint32_t rows;
+    if (!segs_valid(d, text_in, latents, segs, seg_count, &rows, error, error_size)) return 0;
+    if (!segs[seg_count - 1].is_image)
+        return set_error(error, error_size, "ti2i: last run must be image");
+    const uint32_t H = d->cfg.hidden, Z = d->cfg.z_dim, S = slots_of(&d->cfg);
+    const uint32_t t_rows = segs[seg_count - 1].rows, t_base = rows - t_rows;
+    if (!rope_cos || !rope_sin || h3_gpu_tensor_elements(rope_cos) < (size_t)rows * 64 ||
+        h3_gpu_tensor_elements(rope_sin) < (size_t)rows * 64)
+        return set_error(error, error_size, "rope tables must cover %u rows", rows);
+    if (!output || h3_gpu_tensor_elements(output) < (size_t)rows * Z)
+        return set_error(error, error_size, "output too small");
+    struct qw_ti2i_cache *c = &d->ti2i[cache_slot ? 1 : 0];
+    /* qwen_dit.m:1694-1699: the cond rows' inputs do not change across
+     * sampling steps, so a filled cache with the same run layout serves
+     * their K/V and only the target rows are recomputed */
+    const int reuse = c->filled && c->rows == rows && c->target_rows == t_rows &&
+                      c->seg_count == seg_count &&
+                      memcmp(c->segs, segs, sizeof(*segs) * seg_count) == 0;
+    if (!reuse && !cache_alloc(d, c, rows, t_rows, segs, seg_count))
+        return set_error(error, error_size, "ti2i: cache allocation failed");
+    if (!ensure_ws(d, reuse ? t_rows : rows))
+        return set_error(error, error_size, "workspace allocation failed");
+    /* conditioning: row 0 = sigma (target rows), row 1 = t = 0 (the rest) */
+    const float sigmas[2] = {sigma, 0.0f};
+    float feats[512];
+    qw_dit_timestep_features(sigmas, 2, feats);
+    int ok = h3_gpu_tensor_write_f32(d->feat, feats, 512) &&
+             qw_dit_conditioning(d, d->feat, 2, d->temb, d->modulation, d->norm_out_mod, error,
+                                 error_size);
+    const int sh = d->cfg.adaln_shift;
+    if (ok && !reuse) {
+        if (d->joint_rows < rows) {
+            h3_gpu_tensor_free(d->joint);
+            d->joint = h3_gpu_tensor_new_bf16(g, (size_t)rows * H);
+            d->joint_rows = d->joint ? rows : 0;
+        }
+        uint32_t *rm = malloc(sizeof(uint32_t) * rows), *lim = malloc(sizeof(uint32_t) * rows);
+        h3_gpu_tensor *rm_t = NULL, *lim_t = NULL;
+        ok = d->joint && rm && lim;
+        if (ok) {
+            for (uint32_t i = 0; i < rows; i++) rm[i] = i < t_base ? 1u : 0u;
+            qw_dit_prefix_limits(segs, seg_count, lim);
+            rm_t = h3_gpu_tensor_from_u32(g, rm, rows);
+            lim_t = h3_gpu_tensor_from_u32(g, lim, rows);
+            ok = rm_t && lim_t &&
+                 qw_dit_embed_segments(d, text_in, latents, segs, seg_count, d->joint, error,
+                                       error_size);
+        }
+        for (uint32_t l = 0; ok && l < d->cfg.layers; l++)
+            ok = block_run(d, (int)l, d->joint, 1, rows, 0, d->modulation, rope_cos, rope_sin,
+                           rm_t, lim_t, c->k[l], c->v[l], NULL, NULL);
+        ok = ok &&
+             qw_gpu_layer_norm_mod_shift_bf16(g, d->ws_mod, d->joint, d->norm_out_mod, rm_t, rows,
+                                              H, sh ? 2 : 1, 0, sh ? 1 : -1, 1e-6f) &&
+             plain(d, &d->proj_out, output, d->ws_mod, rows, QW_LINEAR_STORE) &&
+             h3_gpu_submit(g) && h3_gpu_begin(g);
+        free(rm);
+        free(lim);
+        h3_gpu_tensor_free(rm_t);
+        h3_gpu_tensor_free(lim_t);
+        if (!ok) {
+            cache_drop(d, c); /* half-filled K/V must not be served later */
+            if (error && !*error) set_error(error, error_size, "%s", h3_gpu_error(g));
+            return error && *error ? 0 : set_error(error, error_size, "ti2i full pass failed");
+        }
+        c->filled = 1;
+        return 1;
+    }
+    if (ok) { /* target-only pass: the target run's rows against the cached K/V */
+        const qw_dit_segment *ts = &segs[seg_count - 1];
+        h3_gpu_tensor *cv = h3_gpu_tensor_view(rope_cos, (size_t)t_base * 64, (size_t)t_rows * 64);
+        h3_gpu_tensor *sv = h3_gpu_tensor_view(rope_sin, (size_t)t_base * 64, (size_t)t_rows * 64);
+        h3_gpu_tensor *ov = h3_gpu_tensor_view(output, (size_t)t_base * Z, (size_t)t_rows * Z);
+        ok = cv && sv && ov &&
+             embed_one(d, NULL, 0, 0, latents, (size_t)ts->src_offset * Z, t_rows, c->th, 0);
+        for (uint32_t l = 0; ok && l < d->cfg.layers; l++) {
+            const qw_kv_cache kvc = {c->k[l], c->v[l], t_base, rows};
+            ok = block_run(d, (int)l, c->th, 1, t_rows, 0, d->modulation, cv, sv, c->row0, NULL,
+                           NULL, NULL, NULL, &kvc);
+        }
+        ok = ok &&
+             qw_gpu_layer_norm_mod_shift_bf16(g, d->ws_mod, c->th, d->norm_out_mod, c->row0,
+                                              t_rows, H, sh ? 2 : 1, 0, sh ? 1 : -1, 1e-6f) &&
+             plain(d, &d->proj_out, ov, d->ws_mod, t_rows, QW_LINEAR_STORE) &&
+             h3_gpu_submit(g) && h3_gpu_begin(g);
+        h3_gpu_tensor_free(cv);
+        h3_gpu_tensor_free(sv);
+        h3_gpu_tensor_free(ov);
+    }
+    (void)S;
+    if (!ok) return error && *error ? 0 : set_error(error, error_size, "ti2i target pass failed: %s",
+                                                    h3_gpu_error(g));
+    return 1;
 }

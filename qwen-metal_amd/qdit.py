@@ -161,6 +161,10 @@ SIGNATURES = {
     "qw_dit_forward_batch_features": (C.c_int, [vp, vp, u32, vp, u32, u32, vp, sz, vp, vp, vp,
                                                 C.c_char_p, sz]),
     "qw_dit_block_profile": (C.c_int, [vp, vp, C.c_int]),
+    "qw_dit_embed_segments": (C.c_int, [vp, vp, vp, vp, u32, vp, C.c_char_p, sz]),
+    "qw_dit_forward_ti2i": (C.c_int, [vp, vp, vp, vp, u32, u32, vp, vp, C.c_float, vp,
+                                      C.c_char_p, sz]),
+    "qw_dit_ti2i_cache_clear": (None, [vp]),
     "qw_latent_grid": (C.c_int, [C.c_int, C.c_int, vp, vp]),
     "qw_calculate_shift": (C.c_double, [C.c_int]),
     "qw_schedule_build": (C.c_int, [C.c_int, C.c_int, vp]),

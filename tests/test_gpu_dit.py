@@ -293,6 +293,74 @@ def test_checkpoint_loader_errors(gpu, qd, oracle, tmp_path, fault):
     assert b"shape" in err.value or b"missing" in err.value
 
 
+# the reference's ti2i fixture layout (tests/test_ti2i_fixture.c:350-355),
+# scaled down: text run, condition image block, text run, target image block
+TI2I_SEGS = [(8, 0, 0), (16, 1, 0), (5, 0, 12), (64, 1, 16)]
+
+
+def _ti2i_call(gpu, qd, dit, ins, segs, slot, sigma, out):
+    import ctypes as C
+    from oracle.oracle import segment_array
+    err = C.create_string_buffer(1024)
+    ok = qd.lib().qw_dit_forward_ti2i(dit.h, ins[0].h, ins[1].h,
+                                      C.cast(segment_array(segs), C.c_void_p), len(segs), slot,
+                                      ins[2].h, ins[3].h, sigma, out.h, err, 1024)
+    return ok, err.value.decode()
+
+
+def test_ti2i_forward_and_step_cache(gpu, qd, oracle):
+    """qw_dit_forward_ti2i (qwen_dit.m:1667-1967). First call: the full pass
+    over the segmented sequence matches the oracle's restatement. Second
+    call, same layout, new sigma: only the target rows are recomputed
+    against the cached K/V; they equal a fresh full pass at that sigma bit
+    for bit, and the other output rows are left as they were."""
+    c = cfg("small", **REF_VARIANT)
+    text = oracle.fill_normal_bf16(20 * c["text_dim"], 8, 930)
+    lat = oracle.fill_normal_bf16(80 * c["z_dim"], 8, 931)
+    rows = sum(r for r, _, _ in TI2I_SEGS)
+    cos, sin = oracle.rope_tables(rows - 64, 8, 8)
+    ins = [gpu.put(text), gpu.put(lat), gpu.put(cos), gpu.put(sin)]
+    dit = qd.Dit(gpu, c, 17)
+    out1 = gpu.new(rows * c["z_dim"], qd.BF16)
+    ok, err = _ti2i_call(gpu, qd, dit, ins, TI2I_SEGS, 0, 0.9, out1)
+    assert ok, err
+    sentinel = np.full(rows * c["z_dim"], 0x3F80, np.uint16)
+    out2 = gpu.put(sentinel)
+    ok, err = _ti2i_call(gpu, qd, dit, ins, TI2I_SEGS, 0, 0.4, out2)  # cached
+    assert ok, err
+    qd.lib().qw_dit_ti2i_cache_clear(dit.h)
+    out3 = gpu.new(rows * c["z_dim"], qd.BF16)
+    ok, err = _ti2i_call(gpu, qd, dit, ins, TI2I_SEGS, 0, 0.4, out3)  # full again
+    assert ok, err
+    gpu.submit()
+    dit.close()
+    g1, g2, g3 = (o.read().reshape(rows, c["z_dim"]) for o in (out1, out2, out3))
+    base = rows - 64
+    assert np.array_equal(g2[base:], g3[base:])
+    assert np.array_equal(g2[:base], sentinel.reshape(rows, -1)[:base])
+    m = oracle.Model(c, 17, c["layers"])
+    f = oracle.bf16_to_f32
+    for sigma, got in ((0.9, g1), (0.4, g3)):
+        ref = m.forward_ti2i(text, 20, lat, 80, TI2I_SEGS, sigma, cos, sin, c["layers"])
+        assert rel_l2(f(got), f(ref)) < 1e-2
+        assert rel_l2(f(got[base:]), f(ref[base:])) < 1e-2
+        assert cosine(f(got[base:]), f(ref[base:])) > 0.9999
+    m.close()
+
+
+def test_ti2i_rejects_bad_layouts(gpu, qd, oracle):
+    c = cfg("small", **REF_VARIANT)
+    ins = [gpu.new(20 * c["text_dim"], qd.BF16), gpu.new(80 * c["z_dim"], qd.BF16),
+           gpu.new(200 * 64, qd.F32), gpu.new(200 * 64, qd.F32)]
+    out = gpu.new(200 * c["z_dim"], qd.BF16)
+    dit = qd.Dit(gpu, c, 1)
+    ok, err = _ti2i_call(gpu, qd, dit, ins, [(16, 1, 0), (8, 0, 0)], 0, 0.5, out)
+    assert not ok and "last run must be image" in err
+    ok, err = _ti2i_call(gpu, qd, dit, ins, [(8, 0, 0), (16, 1, 70)], 0, 0.5, out)
+    assert not ok and "outside its source" in err
+    dit.close()
+
+
 def test_forward_no_text_rows(gpu, qd, oracle):
     """dit_fixture case a topology: image rows only."""
     c = cfg("small", **REF_VARIANT)

@@ -221,3 +221,37 @@ def test_rms_norm_one(oracle):
     oracle.lib().qo_rms_norm_one(out, x, w, 1, 4, 0.0)
     # rms = sqrt(25/4) = 2.5
     assert list(oracle.bf16_to_f32(out)[0]) == [1.203125, 1.6015625, 0.0, 0.0]
+
+
+def test_prefix_limits_layouts(oracle, qd):
+    """qwen_dit.m:1651-1665 by hand on a mixed layout, and the library's own
+    host copy (qw_dit_prefix_limits) agrees."""
+    import ctypes as C
+    segs = [(3, 0, 0), (2, 1, 0), (2, 0, 3), (3, 1, 2)]
+    want = [1, 2, 3, 5, 5, 6, 7, 10, 10, 10]
+    assert oracle.prefix_limits(segs).tolist() == want
+    out = np.zeros(10, np.uint32)
+    qd.lib().qw_dit_prefix_limits(C.cast(oracle.segment_array(segs), C.c_void_p), 4,
+                                  out.ctypes.data)
+    assert out.tolist() == want
+    # [text T, image I] is the t2i table with causal text
+    assert oracle.prefix_limits([(4, 0, 0), (6, 1, 0)]).tolist() == \
+        oracle.t2i_limits(10, 4, True).tolist()
+
+
+def test_ti2i_reduces_to_causal_t2i(oracle):
+    """The ti2i full pass over [text T; target image I] is the t2i forward
+    with causal text rows: same rows, row map (text at t = 0) and limits, so
+    the two oracle paths agree bit for bit."""
+    cfg = dict(hidden=256, heads=2, mlp_width=512, text_dim=256, z_dim=64, layers=2,
+               mlp_act=0, adaln_shift=0, has_bias=0, text_causal=1, int8_weights=0)
+    T, gh, gw = 6, 4, 4
+    I = gh * gw
+    text = oracle.fill_normal_bf16(T * 256, 3, 50)
+    lat = oracle.fill_normal_bf16(I * 64, 3, 51)
+    cos, sin = oracle.rope_tables(T, gh, gw)
+    m = oracle.Model(cfg, 9, 2)
+    a = m.forward(text, T, lat, I, 0.7, cos, sin, 2)
+    b = m.forward_ti2i(text, T, lat, I, [(T, 0, 0), (I, 1, 0)], 0.7, cos, sin, 2)
+    m.close()
+    assert np.array_equal(a, b)
