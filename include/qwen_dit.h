@@ -163,6 +163,32 @@ int qw_dit_forward_ti2i(qw_dit *dit, const h3_gpu_tensor *text_in,
                         h3_gpu_tensor *output, char *error,
                         size_t error_size);
 
+/* reference qwen_dit.h:42-82: LoRA adapters (single safetensors files,
+ * rank-r pairs transformer_blocks.N.<module>.lora_A / .lora_B.default.weight
+ * for the modules attn.to_q, .to_k, .to_v, .to_out.0, img_mlp.gate_layer,
+ * .proj, .out; A bf16 [r, in], B bf16 [out, r]). Adapters stack:
+ * W' = RNE_bf16(fp32(W) + sum_a scale_a B_a A_a), rebuilt on the device
+ * from the kept base weights on every change (one rounding, order
+ * independent); missing targets are skipped; no lora_alpha (scale is the
+ * caller's strength). Any change drops the ti2i caches. A failed rebuild
+ * resets the stack to none. Adapters fuse into bf16 block weights of the
+ * reference architecture: an int8 or GELU/bias model refuses them. */
+#define QW_DIT_MAX_LORA 8
+/* new path: appended, or an existing path's scale updated; fails without
+ * a state change on an unreadable file, no matching tensor or a full stack */
+int qw_dit_apply_lora(qw_dit *dit, const char *path, float scale,
+                      char *error, size_t error_size);
+/* NULL or "" removes all; an unknown path is a no-op */
+int qw_dit_remove_lora(qw_dit *dit, const char *path, char *error,
+                       size_t error_size);
+/* replaces the single active adapter; a broken file leaves it active */
+int qw_dit_switch_lora(qw_dit *dit, const char *path, float scale,
+                       char *error, size_t error_size);
+int qw_dit_clear_lora(qw_dit *dit, char *error, size_t error_size);
+int qw_dit_lora_count(const qw_dit *dit);
+const char *qw_dit_lora_path_at(const qw_dit *dit, int index);
+float qw_dit_lora_scale_at(const qw_dit *dit, int index);
+
 /* reference qwen_dit.h:35-40: drop both ti2i caches (they hold one
  * request's conditioning; call at the end of every ti2i generation). */
 void qw_dit_ti2i_cache_clear(qw_dit *dit);

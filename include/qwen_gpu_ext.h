@@ -188,6 +188,24 @@ int qw_gpu_cfg_euler_f32(h3_gpu *gpu, h3_gpu_tensor *x, const h3_gpu_tensor *pos
                          size_t pos_offset, const h3_gpu_tensor *neg,
                          size_t neg_offset, size_t count, float dt, float cfg);
 
+#define QW_GPU_LORA_MAX_RANK 256
+#define QW_GPU_LORA_MAX_TERMS 24
+/* LoRA weight fusion (qwen_dit.m:535-1010):
+ *   out = RNE_bf16(fp32(base) + sum_t scale_t * (B_t @ A_t))
+ * base, out bf16 [rows, cols] (may not alias); term t adds to fused rows
+ * [row0, row0 + rows) with A bf16 [rank, cols] and B bf16 [rows, rank],
+ * rank <= 256, at most 24 terms, applied in order with one final rounding.
+ * No counterpart in the reference (which fuses on the host). */
+typedef struct {
+    const h3_gpu_tensor *a, *b;
+    uint32_t row0, rows, rank;
+    float scale;
+} qw_lora_term_desc;
+int qw_gpu_lora_fuse_bf16(h3_gpu *gpu, h3_gpu_tensor *out,
+                          const h3_gpu_tensor *base, uint32_t rows,
+                          uint32_t cols, const qw_lora_term_desc *terms,
+                          uint32_t nterms);
+
 /* Strided row copy: rows x row_elems of dtype-size elements. */
 int qw_gpu_copy_rows(h3_gpu *gpu, h3_gpu_tensor *dst, size_t dst_offset,
                      uint32_t dst_stride, const h3_gpu_tensor *src,

@@ -29,7 +29,7 @@ enum {
     K_GEMM_BF16_STORE_W8, K_GEMM_BF16_GELU_W8, K_GEMM_BF16_GATE_W8,
     K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8,
     K_GEMM_BF16_STORE_R, K_GEMM_BF16_GELU_R, K_GEMM_BF16_GATE_R,
-    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_COUNT
+    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_bf16", "qw_rms_norm_one_bf16", "qw_qk_norm_rope_bf16",
@@ -42,7 +42,7 @@ static const char *k_names[K_COUNT] = {
     "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8",
     "qw_gemm_bf16_store_r", "qw_gemm_bf16_gelu_r", "qw_gemm_bf16_gate_r",
     "qw_gemm_i8_store_r", "qw_gemm_i8_gelu_r", "qw_gemm_i8_gate_r", "qw_widen_i8_bf16",
-    "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32"};
+    "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16"};
 
 struct h3_gpu {
     int device;
@@ -566,6 +566,37 @@ extern "C" int qw_gpu_cfg_euler_f32(h3_gpu *g, h3_gpu_tensor *x, const h3_gpu_te
     qw_euler_args a = {(float *)x->ptr, (const uint16_t *)pos->ptr + pos_offset,
                        neg ? (const uint16_t *)neg->ptr + neg_offset : NULL, count, dt, cfg};
     return launch(g, K_EULER, dim3(blocks_for(count, 256)), dim3(256), a);
+}
+
+extern "C" int qw_gpu_lora_fuse_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *base,
+                                     uint32_t rows, uint32_t cols, const qw_lora_term_desc *terms,
+                                     uint32_t nterms) {
+    if (!g) return 0;
+    REQ_DT(out, H3_GPU_BF16, "lora out");
+    REQ_DT(base, H3_GPU_BF16, "lora base");
+    if (!fits(out, 0, (size_t)rows * cols) || !fits(base, 0, (size_t)rows * cols))
+        return fail(g, "lora: tensors smaller than %u x %u", rows, cols);
+    if (nterms > QW_LORA_MAX_TERMS) return fail(g, "lora: %u terms (max %d)", nterms, QW_LORA_MAX_TERMS);
+    qw_lora_args a;
+    memset(&a, 0, sizeof(a));
+    a.out = (uint16_t *)out->ptr;
+    a.base = (const uint16_t *)base->ptr;
+    a.rows = rows;
+    a.cols = cols;
+    a.nterms = nterms;
+    for (uint32_t t = 0; t < nterms; t++) {
+        const qw_lora_term_desc *d = &terms[t];
+        REQ_DT(d->a, H3_GPU_BF16, "lora A");
+        REQ_DT(d->b, H3_GPU_BF16, "lora B");
+        if (!d->rank || d->rank > QW_LORA_MAX_RANK)
+            return fail(g, "lora: rank %u outside [1, %d]", d->rank, QW_LORA_MAX_RANK);
+        if ((uint64_t)d->row0 + d->rows > rows) return fail(g, "lora: term rows outside the weight");
+        if (!fits(d->a, 0, (size_t)d->rank * cols) || !fits(d->b, 0, (size_t)d->rows * d->rank))
+            return fail(g, "lora: A or B smaller than its shape");
+        a.terms[t] = qw_lora_term{(const uint16_t *)d->a->ptr, (const uint16_t *)d->b->ptr, d->row0,
+                                  d->rows, d->rank, d->scale};
+    }
+    return launch(g, K_LORA, dim3((cols + 63) / 64, (rows + 63) / 64), dim3(256), a);
 }
 
 extern "C" int h3_gpu_gate_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gpu_tensor *res,

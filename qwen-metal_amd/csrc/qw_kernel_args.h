@@ -172,4 +172,20 @@ typedef struct {
     float scale_log2; /* softmax scale * log2(e) */
 } qw_attn_args;
 
+/* LoRA fusion: out[rows, cols] = RNE(fp32(base) + sum of the terms) */
+#define QW_LORA_MAX_RANK 256
+#define QW_LORA_MAX_TERMS 24
+typedef struct {
+    const uint16_t *a; /* bf16 [rank, cols] */
+    const uint16_t *b; /* bf16 [rows, rank]: fused rows [row0, row0 + rows) */
+    uint32_t row0, rows, rank;
+    float scale;
+} qw_lora_term;
+typedef struct {
+    uint16_t *out;
+    const uint16_t *base;
+    uint32_t rows, cols, nterms;
+    qw_lora_term terms[QW_LORA_MAX_TERMS];
+} qw_lora_args;
+
 #endif

@@ -14,6 +14,7 @@
  *     M = batch * rows, attention has a batch grid dimension.
  * Rounding points are the reference kernels' (bf16 RNE at each reference
  * op boundary). */
+#define _DEFAULT_SOURCE /* strdup */
 #include "../../include/qwen_dit.h"
 
 #include <math.h>
@@ -61,6 +62,17 @@ struct qw_dit {
     uint32_t rm_rows, rm_text, rm_batch;
     int profile;
     double prof_ms[P_COUNT];
+    /* LoRA adapters, in stack order; while any is active, base[4 l + j]
+     * keeps layer l's base weight j (qkv, out, fc1, fc2) and the layer
+     * holds the fused copy */
+    struct qw_lora {
+        char *path;
+        float scale;
+        uint32_t rank;
+        h3_st_header header;
+    } lora[QW_DIT_MAX_LORA];
+    int n_lora;
+    h3_gpu_tensor **lora_base;
     /* ti2i cross-step caches (slot 0: guided branch, 1: CFG negative) */
     struct qw_ti2i_cache {
         uint32_t rows, target_rows, seg_count;
@@ -406,8 +418,283 @@ qw_dit *qw_dit_create(h3_gpu *gpu, const char *model_dir, int layers, char *erro
     return qw_dit_load(gpu, model_dir, &cfg, error, error_size);
 }
 
+/* ---------------------------------------------------------------------- */
+/* LoRA (qwen_dit.m:535-1010)                                              */
+
+/* The adapter targets of block weight j: module name, first fused row,
+ * rows (keys: transformer_blocks.N.<module>.lora_{A,B}.default.weight). */
+typedef struct {
+    const char *module;
+    uint32_t row0, rows;
+} lora_target;
+
+static int lora_targets(const qw_dit *d, int j, lora_target *t, uint32_t *cols) {
+    const uint32_t H = d->cfg.hidden, F = d->cfg.mlp_width;
+    switch (j) {
+    case 0:
+        t[0] = (lora_target){"attn.to_q", 0, H};
+        t[1] = (lora_target){"attn.to_k", H, H};
+        t[2] = (lora_target){"attn.to_v", 2 * H, H};
+        *cols = H;
+        return 3;
+    case 1:
+        t[0] = (lora_target){"attn.to_out.0", 0, H};
+        *cols = H;
+        return 1;
+    case 2:
+        t[0] = (lora_target){"img_mlp.gate_layer", 0, F};
+        t[1] = (lora_target){"img_mlp.proj", F, F};
+        *cols = H;
+        return 2;
+    default:
+        t[0] = (lora_target){"img_mlp.out", 0, H};
+        *cols = F;
+        return 1;
+    }
+}
+
+static qw_lin *layer_lin(qw_layer *L, int j) {
+    return j == 0 ? &L->qkv : j == 1 ? &L->out : j == 2 ? &L->fc1 : &L->fc2;
+}
+
+/* every adapter dropped, base weights back in the layers, fused copies and
+ * ti2i caches (made with the old weights) freed */
+static void lora_reset(qw_dit *d) {
+    if (d->lora_base) {
+        for (uint32_t l = 0; l < d->cfg.layers; l++)
+            for (int j = 0; j < 4; j++) {
+                qw_lin *w = layer_lin(&d->layer[l], j);
+                h3_gpu_tensor *base = d->lora_base[4 * l + j];
+                if (base && w->w != base) {
+                    h3_gpu_tensor_free(w->w);
+                    w->w = base;
+                }
+            }
+        free(d->lora_base);
+        d->lora_base = NULL;
+    }
+    for (int i = 0; i < d->n_lora; i++) {
+        free(d->lora[i].path);
+        h3_st_free_header(&d->lora[i].header);
+    }
+    d->n_lora = 0;
+    qw_dit_ti2i_cache_clear(d);
+}
+
+/* A bf16 [rows, cols] matrix of an adapter: 1 read into a new device
+ * tensor, 0 absent (partial adapters are allowed), -1 broken */
+static int lora_matrix(qw_dit *d, const h3_st_header *h, const char *key, uint32_t rows,
+                       uint32_t cols, h3_gpu_tensor **out, char *error, size_t error_size) {
+    *out = NULL;
+    const h3_st_tensor *t = h3_st_find(h, key);
+    if (!t) return 0;
+    if (t->dtype != H3_DTYPE_BF16 || t->ndim != 2 || t->shape[0] != rows || t->shape[1] != cols) {
+        set_error(error, error_size, "lora tensor %s: expected bf16 [%u x %u]", key, rows, cols);
+        return -1;
+    }
+    const size_t n = (size_t)rows * cols;
+    uint16_t *host = malloc(sizeof(uint16_t) * (n ? n : 1));
+    *out = h3_gpu_tensor_new_bf16(d->gpu, n);
+    int ok = host && *out && h3_st_read_data(h, t, host, sizeof(uint16_t) * n, error, error_size) &&
+             h3_gpu_tensor_write_bf16(*out, host, n);
+    free(host);
+    if (!ok) {
+        h3_gpu_tensor_free(*out);
+        *out = NULL;
+        if (error && !*error) set_error(error, error_size, "lora tensor %s: read failed", key);
+        return -1;
+    }
+    return 1;
+}
+
+/* Every fused weight rebuilt from the kept base in one pass (so the order
+ * of apply / remove / scale changes does not matter and nothing rounds
+ * twice). On failure the adapter state is reset to none. */
+static int lora_rebuild(qw_dit *d, char *error, size_t error_size) {
+    h3_gpu *g = d->gpu;
+    int ok = 1;
+    if (!d->lora_base) {
+        d->lora_base = calloc((size_t)4 * d->cfg.layers, sizeof(h3_gpu_tensor *));
+        ok = d->lora_base != NULL;
+        for (uint32_t l = 0; ok && l < d->cfg.layers; l++)
+            for (int j = 0; ok && j < 4; j++) {
+                qw_lin *w = layer_lin(&d->layer[l], j);
+                h3_gpu_tensor *fused = h3_gpu_tensor_new_bf16(g, (size_t)w->n * w->k);
+                ok = fused != NULL;
+                if (ok) {
+                    d->lora_base[4 * l + j] = w->w;
+                    w->w = fused;
+                }
+            }
+        if (!ok) set_error(error, error_size, "lora: out of memory for the fused weights");
+    }
+    for (uint32_t l = 0; ok && l < d->cfg.layers; l++)
+        for (int j = 0; ok && j < 4; j++) {
+            lora_target tg[3];
+            uint32_t cols;
+            const int nt = lora_targets(d, j, tg, &cols);
+            qw_lora_term_desc terms[QW_GPU_LORA_MAX_TERMS];
+            h3_gpu_tensor *held[2 * QW_GPU_LORA_MAX_TERMS];
+            uint32_t n = 0, nh = 0;
+            for (int a = 0; ok && a < d->n_lora; a++)
+                for (int t = 0; ok && t < nt; t++) {
+                    char ka[192], kb[192];
+                    snprintf(ka, sizeof(ka), "transformer_blocks.%u.%s.lora_A.default.weight", l,
+                             tg[t].module);
+                    snprintf(kb, sizeof(kb), "transformer_blocks.%u.%s.lora_B.default.weight", l,
+                             tg[t].module);
+                    h3_gpu_tensor *A, *B;
+                    const int ra = lora_matrix(d, &d->lora[a].header, ka, d->lora[a].rank, cols,
+                                               &A, error, error_size);
+                    if (ra <= 0) {
+                        ok = ra == 0;
+                        continue;
+                    }
+                    held[nh++] = A;
+                    const int rb = lora_matrix(d, &d->lora[a].header, kb, tg[t].rows,
+                                               d->lora[a].rank, &B, error, error_size);
+                    if (rb <= 0) {
+                        ok = rb == 0;
+                        continue;
+                    }
+                    held[nh++] = B;
+                    terms[n++] = (qw_lora_term_desc){A, B, tg[t].row0, tg[t].rows, d->lora[a].rank,
+                                                     d->lora[a].scale};
+                }
+            qw_lin *w = layer_lin(&d->layer[l], j);
+            ok = ok && qw_gpu_lora_fuse_bf16(g, w->w, d->lora_base[4 * l + j], w->n, w->k, terms, n);
+            if (!ok && error && !*error) set_error(error, error_size, "lora: %s", h3_gpu_error(g));
+            for (uint32_t i = 0; i < nh; i++) h3_gpu_tensor_free(held[i]); /* waits for the fuse */
+        }
+    qw_dit_ti2i_cache_clear(d); /* cached K/V came from the previous weights */
+    if (!ok) lora_reset(d);
+    return ok;
+}
+
+/* header readable, a rank (first bf16 2-D lora_A: its rows), and at least
+ * one key that matches a block target */
+static int lora_open(const qw_dit *d, const char *path, h3_st_header *h, uint32_t *rank,
+                     char *error, size_t error_size) {
+    if (!h3_st_read_header(path, h, error, error_size)) return 0;
+    *rank = 0;
+    for (size_t i = 0; i < h->tensor_count && !*rank; i++)
+        if (h->tensors[i].dtype == H3_DTYPE_BF16 && h->tensors[i].ndim == 2 &&
+            strstr(h->tensors[i].name, ".lora_A.default.weight"))
+            *rank = (uint32_t)h->tensors[i].shape[0];
+    if (!*rank || *rank > QW_GPU_LORA_MAX_RANK) {
+        h3_st_free_header(h);
+        return set_error(error, error_size, "lora file carries no bf16 lora_A matrices of rank "
+                         "1..%d: %s", QW_GPU_LORA_MAX_RANK, path);
+    }
+    for (uint32_t l = 0; l < d->cfg.layers; l++)
+        for (int j = 0; j < 4; j++) {
+            lora_target tg[3];
+            uint32_t cols;
+            const int nt = lora_targets(d, j, tg, &cols);
+            for (int t = 0; t < nt; t++) {
+                char key[192];
+                snprintf(key, sizeof(key), "transformer_blocks.%u.%s.lora_A.default.weight", l,
+                         tg[t].module);
+                if (h3_st_find(h, key)) return 1;
+            }
+        }
+    h3_st_free_header(h);
+    return set_error(error, error_size, "lora matched no checkpoint tensors: %s", path);
+}
+
+static int lora_supported(const qw_dit *d, char *error, size_t error_size) {
+    if (d->cfg.int8_weights)
+        return set_error(error, error_size, "lora: the block weights are int8; adapters fuse into "
+                         "bf16 weights");
+    if (d->cfg.mlp_act != QW_MLP_SWIGLU || d->cfg.has_bias)
+        return set_error(error, error_size, "lora: adapters target the reference architecture "
+                         "(SwiGLU MLP, no biases)");
+    return 1;
+}
+
+int qw_dit_apply_lora(qw_dit *d, const char *path, float scale, char *error, size_t error_size) {
+    if (error && error_size) error[0] = '\0';
+    if (!d) return set_error(error, error_size, "no dit");
+    if (!path || !*path) return set_error(error, error_size, "lora path is required");
+    if (!lora_supported(d, error, error_size)) return 0;
+    for (int i = 0; i < d->n_lora; i++)
+        if (strcmp(d->lora[i].path, path) == 0) { /* known adapter: new scale */
+            d->lora[i].scale = scale;
+            return lora_rebuild(d, error, error_size);
+        }
+    if (d->n_lora >= QW_DIT_MAX_LORA)
+        return set_error(error, error_size, "lora stack is full (%d adapters)", QW_DIT_MAX_LORA);
+    h3_st_header h;
+    uint32_t rank;
+    if (!lora_open(d, path, &h, &rank, error, error_size)) return 0;
+    char *copy = strdup(path);
+    if (!copy) {
+        h3_st_free_header(&h);
+        return set_error(error, error_size, "out of memory");
+    }
+    d->lora[d->n_lora] = (struct qw_lora){copy, scale, rank, h};
+    d->n_lora++;
+    return lora_rebuild(d, error, error_size);
+}
+
+int qw_dit_switch_lora(qw_dit *d, const char *path, float scale, char *error,
+                       size_t error_size) {
+    if (error && error_size) error[0] = '\0';
+    if (!d || !path || !*path) return set_error(error, error_size, "lora path is required");
+    if (d->n_lora != 1)
+        return set_error(error, error_size, "switch requires exactly one active adapter");
+    if (strcmp(d->lora[0].path, path) == 0) return qw_dit_apply_lora(d, path, scale, error, error_size);
+    h3_st_header h;
+    uint32_t rank;
+    if (!lora_open(d, path, &h, &rank, error, error_size)) return 0; /* old one stays */
+    char *copy = strdup(path);
+    if (!copy) {
+        h3_st_free_header(&h);
+        return set_error(error, error_size, "out of memory");
+    }
+    free(d->lora[0].path);
+    h3_st_free_header(&d->lora[0].header);
+    d->lora[0] = (struct qw_lora){copy, scale, rank, h};
+    return lora_rebuild(d, error, error_size);
+}
+
+int qw_dit_remove_lora(qw_dit *d, const char *path, char *error, size_t error_size) {
+    if (!d) return set_error(error, error_size, "no dit");
+    if (!path || !*path) return qw_dit_clear_lora(d, error, error_size);
+    for (int i = 0; i < d->n_lora; i++)
+        if (strcmp(d->lora[i].path, path) == 0) {
+            free(d->lora[i].path);
+            h3_st_free_header(&d->lora[i].header);
+            memmove(&d->lora[i], &d->lora[i + 1], sizeof(d->lora[0]) * (size_t)(d->n_lora - i - 1));
+            d->n_lora--;
+            if (!d->n_lora) {
+                lora_reset(d);
+                return 1;
+            }
+            return lora_rebuild(d, error, error_size);
+        }
+    return 1; /* unknown path: nothing to remove */
+}
+
+int qw_dit_clear_lora(qw_dit *d, char *error, size_t error_size) {
+    if (!d) return set_error(error, error_size, "no dit");
+    lora_reset(d);
+    return 1;
+}
+
+int qw_dit_lora_count(const qw_dit *d) { return d ? d->n_lora : 0; }
+
+const char *qw_dit_lora_path_at(const qw_dit *d, int index) {
+    return d && index >= 0 && index < d->n_lora ? d->lora[index].path : NULL;
+}
+
+float qw_dit_lora_scale_at(const qw_dit *d, int index) {
+    return d && index >= 0 && index < d->n_lora ? d->lora[index].scale : 0.0f;
+}
+
 void qw_dit_free(qw_dit *d) {
     if (!d) return;
+    lora_reset(d);
     if (d->layer)
         for (uint32_t l = 0; l < d->cfg.layers; l++) {
             lin_free(&d->layer[l].qkv);

@@ -5,3 +5,4 @@
 #include "kernels/gemm.h"
 #include "kernels/gemm_ring.h"
 #include "kernels/attention.h"
+#include "kernels/lora.h"

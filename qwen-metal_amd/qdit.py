@@ -161,6 +161,14 @@ SIGNATURES = {
     "qw_dit_forward_batch_features": (C.c_int, [vp, vp, u32, vp, u32, u32, vp, sz, vp, vp, vp,
                                                 C.c_char_p, sz]),
     "qw_dit_block_profile": (C.c_int, [vp, vp, C.c_int]),
+    "qw_dit_apply_lora": (C.c_int, [vp, C.c_char_p, C.c_float, C.c_char_p, sz]),
+    "qw_dit_remove_lora": (C.c_int, [vp, C.c_char_p, C.c_char_p, sz]),
+    "qw_dit_switch_lora": (C.c_int, [vp, C.c_char_p, C.c_float, C.c_char_p, sz]),
+    "qw_dit_clear_lora": (C.c_int, [vp, C.c_char_p, sz]),
+    "qw_dit_lora_count": (C.c_int, [vp]),
+    "qw_dit_lora_path_at": (C.c_char_p, [vp, C.c_int]),
+    "qw_dit_lora_scale_at": (C.c_float, [vp, C.c_int]),
+    "qw_gpu_lora_fuse_bf16": (C.c_int, [vp, vp, vp, u32, u32, vp, u32]),
     "qw_dit_embed_segments": (C.c_int, [vp, vp, vp, vp, u32, vp, C.c_char_p, sz]),
     "qw_dit_forward_ti2i": (C.c_int, [vp, vp, vp, vp, u32, u32, vp, vp, C.c_float, vp,
                                       C.c_char_p, sz]),

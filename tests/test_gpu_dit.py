@@ -8,7 +8,7 @@ bf16 noise band; the velocity after the full depth relL2 <= 1e-2."""
 import numpy as np
 import pytest
 
-from conftest import cosine, rel_l2
+from conftest import cosine, rel_l2, ulp_diff
 
 pytestmark = pytest.mark.gpu
 
@@ -459,3 +459,130 @@ def test_block_prefix_limits(gpu, qd, oracle):
 def _release_uploads(gpu):
     yield
     gpu.release()
+
+
+def _lora_file(path, entries):
+    """entries: {(layer, module): (A [r, in], B [out, r]) as float32}"""
+    torch = pytest.importorskip("torch")
+    st = pytest.importorskip("safetensors.torch")
+    t = {}
+    for (l, mod), (a, b) in entries.items():
+        p = f"transformer_blocks.{l}.{mod}"
+        t[p + ".lora_A.default.weight"] = torch.from_numpy(a).bfloat16()
+        t[p + ".lora_B.default.weight"] = torch.from_numpy(b).bfloat16()
+    st.save_file(t, str(path))
+    return str(path).encode()
+
+
+def _bf16_round(x):
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    return ((b + np.uint32(0x7FFF) + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_lora_fusion_stack(gpu, qd, oracle, tmp_path):
+    """qw_dit_apply/remove/switch/clear_lora (qwen_dit.m:535-1010): the fused
+    block weights are RNE_bf16(fp32(W) + sum_a scale_a B_a A_a) over the
+    adapters present (partial adapters skip their missing targets), within
+    one bf16 ulp of a float64 restatement; clear restores the base weights
+    bit for bit; a broken switch leaves the adapter active."""
+    import ctypes as C
+    c = cfg("small", **REF_VARIANT)
+    H, F = c["hidden"], c["mlp_width"]
+    rng = np.random.default_rng(7)
+
+    def pair(r, out, inp):
+        return (rng.normal(0, 0.05, (r, inp)).astype(np.float32),
+                rng.normal(0, 0.05, (out, r)).astype(np.float32))
+    ad1 = {(0, "attn.to_q"): pair(4, H, H), (0, "attn.to_v"): pair(4, H, H),
+           (2, "attn.to_out.0"): pair(4, H, H), (2, "img_mlp.gate_layer"): pair(4, F, H),
+           (0, "img_mlp.out"): pair(4, H, F)}
+    ad2 = {(1, "attn.to_k"): pair(8, H, H), (1, "img_mlp.proj"): pair(8, F, H),
+           (0, "attn.to_q"): pair(8, H, H)}
+    p1, p2 = _lora_file(tmp_path / "a.safetensors", ad1), _lora_file(tmp_path / "b.safetensors", ad2)
+    (tmp_path / "none.safetensors").write_bytes(b"")
+    _lora_file(tmp_path / "other.safetensors", {(0, "attn.add_q_proj"): pair(4, H, H)})
+    dit = qd.Dit(gpu, c, 3)
+    L = qd.lib()
+    # field -> (block field id, rows, cols, [(module, row0)])
+    fields = {0: (0, 3 * H, H, [("attn.to_q", 0), ("attn.to_k", H), ("attn.to_v", 2 * H)]),
+              1: (3, H, H, [("attn.to_out.0", 0)]),
+              2: (4, 2 * F, H, [("img_mlp.gate_layer", 0), ("img_mlp.proj", F)]),
+              3: (5, H, F, [("img_mlp.out", 0)])}
+
+    def weights():
+        gpu.submit()
+        out = {}
+        for l in range(c["layers"]):
+            for j, (fid, rows, cols, _) in fields.items():
+                buf = np.empty(rows * cols, np.uint16)
+                assert L.h3_gpu_tensor_read_bf16(L.qw_dit_block_tensor(dit.h, l, fid),
+                                                 buf.ctypes.data, buf.size)
+                out[(l, j)] = buf.reshape(rows, cols)
+        return out
+
+    def expect(base, stack):
+        """float64 sum and the magnitude sum |W| + sum |s| |B| |A| that
+        bounds the fp32 accumulation error"""
+        f = oracle.bf16_to_f32
+        want = {}
+        for (l, j), w in base.items():
+            _, rows, cols, mods = fields[j]
+            acc = f(w).astype(np.float64)
+            mag = np.abs(acc)
+            for ad, s in stack:
+                for mod, row0 in mods:
+                    if (l, mod) in ad:
+                        a, b = ad[(l, mod)]
+                        a = f(_bf16_round(a)).astype(np.float64)
+                        b = f(_bf16_round(b)).astype(np.float64)
+                        acc[row0:row0 + b.shape[0]] += s * (b @ a)
+                        mag[row0:row0 + b.shape[0]] += abs(s) * (np.abs(b) @ np.abs(a))
+            want[(l, j)] = (_bf16_round(acc.astype(np.float32)), mag)
+        return want
+
+    def check(stack):
+        """one rounding of an fp32 sum: within 1 bf16 ulp of the float64
+        result, except where the sum cancels and the fp32 accumulation
+        error (a few 2^-24 |terms|) spans more bf16 ulps of a tiny result"""
+        got, want = weights(), expect(base, stack)
+        f = oracle.bf16_to_f32
+        for key in got:
+            w, mag = want[key]
+            d = ulp_diff(got[key], w)
+            diff = np.abs(f(got[key]).astype(np.float64) - f(w))
+            ok = (d <= 1) | (diff <= 2.0 ** -20 * mag)
+            assert ok.all() and np.mean(d == 0) > 0.99, (key, d.max(), np.mean(d == 0))
+
+    def call(fn, *args):
+        err = C.create_string_buffer(512)
+        ok = fn(dit.h, *args, err, 512)
+        return ok, err.value.decode()
+
+    base = weights()
+    assert call(L.qw_dit_apply_lora, p1, 0.7)[0]
+    check([(ad1, 0.7)])
+    assert call(L.qw_dit_apply_lora, p2, 1.3)[0]
+    check([(ad1, 0.7), (ad2, 1.3)])
+    assert call(L.qw_dit_apply_lora, p1, -0.5)[0]  # same path: new scale, stack order kept
+    check([(ad1, -0.5), (ad2, 1.3)])
+    assert L.qw_dit_lora_count(dit.h) == 2 and L.qw_dit_lora_scale_at(dit.h, 0) == -0.5
+    assert call(L.qw_dit_remove_lora, p1)[0]
+    check([(ad2, 1.3)])
+    ok, err = call(L.qw_dit_switch_lora, str(tmp_path / "none.safetensors").encode(), 1.0)
+    assert not ok and err
+    check([(ad2, 1.3)])
+    assert call(L.qw_dit_switch_lora, p1, 0.2)[0]
+    check([(ad1, 0.2)])
+    assert L.qw_dit_lora_path_at(dit.h, 0) == p1
+    ok, err = call(L.qw_dit_apply_lora, str(tmp_path / "other.safetensors").encode(), 1.0)
+    assert not ok and "matched no" in err
+    assert L.qw_dit_lora_count(dit.h) == 1
+    assert call(L.qw_dit_clear_lora)[0]
+    got = weights()
+    assert all(np.array_equal(got[k], base[k]) for k in base)
+    assert L.qw_dit_lora_count(dit.h) == 0
+    dit.close()
+    q8 = qd.Dit(gpu, dict(c, int8_weights=1), 3)
+    err = C.create_string_buffer(512)
+    assert not L.qw_dit_apply_lora(q8.h, p1, 1.0, err, 512) and b"int8" in err.value
+    q8.close()
