@@ -86,13 +86,14 @@ int qw_gpu_layer_norm_mod_shift_bf16(h3_gpu *gpu, h3_gpu_tensor *output,
                                      uint32_t slots, uint32_t scale_slot,
                                      int32_t shift_slot, float epsilon);
 
-enum { QW_LINEAR_STORE = 0, QW_LINEAR_GELU = 1, QW_LINEAR_GATE = 2 };
+enum { QW_LINEAR_STORE = 0, QW_LINEAR_GELU = 1, QW_LINEAR_GATE = 2, QW_LINEAR_QKNORM = 3 };
 
 /* One GEMM with a fused epilogue, on sub-ranges of tensors:
  *   y = bf16( X W^T * wscale + bias )                  (STORE)
  *   y = bf16( gelu_tanh( bf16(X W^T * wscale + bias) ) ) (GELU)
  *   out = bf16( out + bf16(X W^T * wscale + bias) * gate ) (GATE, in place;
  *         gate row = row_map[r], columns gate_slot*cols..)
+ *   y, then per-head RMS norm + RoPE on the q and k thirds (QKNORM)
  * weight is bf16 [cols, k] or int8 [cols, k] (then wscale f32 [cols] is
  * required; without wscale a bf16 weight is unscaled). Offsets/strides are
  * in elements; k must be a multiple of 64. An int8 linear of 512 or more
@@ -114,6 +115,13 @@ typedef struct {
     const h3_gpu_tensor *modulation; /* GATE */
     const h3_gpu_tensor *row_map;    /* GATE */
     uint32_t slots, gate_slot;       /* GATE: row stride slots*cols */
+    /* QKNORM: the fused q|k|v projection (cols = 3 heads 128, out_offset 0)
+     * with qw_gpu_qk_norm_rope_bf16 applied to its q and k columns in the
+     * epilogue (same result as the two calls); the RoPE table row is
+     * row % rope_rows */
+    const h3_gpu_tensor *norm_q, *norm_k, *rope_cos, *rope_sin;
+    uint32_t rope_rows;
+    float eps;
 } qw_linear_desc;
 int qw_gpu_linear(h3_gpu *gpu, const qw_linear_desc *desc);
 

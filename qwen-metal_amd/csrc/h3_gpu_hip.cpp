@@ -27,7 +27,8 @@ enum {
     K_GEMM_BF16_STORE, K_GEMM_BF16_GELU, K_GEMM_BF16_GATE,
     K_GEMM_I8_STORE, K_GEMM_I8_GELU, K_GEMM_I8_GATE,
     K_GEMM_BF16_STORE_W8, K_GEMM_BF16_GELU_W8, K_GEMM_BF16_GATE_W8,
-    K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8,
+    K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_GEMM_BF16_QKN_W8,
+    K_GEMM_I8_QKN_W8,
     K_GEMM_BF16_STORE_R, K_GEMM_BF16_GELU_R, K_GEMM_BF16_GATE_R,
     K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA, K_COUNT
 };
@@ -40,6 +41,7 @@ static const char *k_names[K_COUNT] = {
     "qw_gemm_i8_store", "qw_gemm_i8_gelu", "qw_gemm_i8_gate",
     "qw_gemm_bf16_store_w8", "qw_gemm_bf16_gelu_w8", "qw_gemm_bf16_gate_w8",
     "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8",
+    "qw_gemm_bf16_qkn_w8", "qw_gemm_i8_qkn_w8",
     "qw_gemm_bf16_store_r", "qw_gemm_bf16_gelu_r", "qw_gemm_bf16_gate_r",
     "qw_gemm_i8_store_r", "qw_gemm_i8_gelu_r", "qw_gemm_i8_gate_r", "qw_widen_i8_bf16",
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16"};
@@ -880,6 +882,20 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
         if (d->modulation->elements < gate_stride) return fail(g, "linear: modulation too small");
         gate = (const uint16_t *)d->modulation->ptr + (size_t)d->gate_slot * d->cols;
         row_map = (const uint32_t *)d->row_map->ptr;
+    } else if (d->epilogue == QW_LINEAR_QKNORM) {
+        REQ_DT(d->norm_q, H3_GPU_BF16, "linear qk norm_q");
+        REQ_DT(d->norm_k, H3_GPU_BF16, "linear qk norm_k");
+        REQ_DT(d->rope_cos, H3_GPU_F32, "linear qk rope cos");
+        REQ_DT(d->rope_sin, H3_GPU_F32, "linear qk rope sin");
+        if (d->cols % 384 || d->out_offset || d->ldc % 8)
+            return fail(g, "linear qk: cols must be q|k|v heads of 128, output at offset 0");
+        if (d->norm_q->elements < 128 || d->norm_k->elements < 128 || !d->rope_rows ||
+            !fits(d->rope_cos, 0, (size_t)d->rope_rows * 64) ||
+            !fits(d->rope_sin, 0, (size_t)d->rope_rows * 64))
+            return fail(g, "linear qk: norm weights or rope tables too small");
+        if (((uintptr_t)d->norm_q->ptr | (uintptr_t)d->norm_k->ptr | (uintptr_t)d->rope_cos->ptr |
+             (uintptr_t)d->rope_sin->ptr | (uintptr_t)d->out->ptr) % 16)
+            return fail(g, "linear qk: tensors must be 16-byte aligned");
     } else if (d->epilogue != QW_LINEAR_STORE && d->epilogue != QW_LINEAR_GELU) {
         return fail(g, "linear: unknown epilogue %d", d->epilogue);
     }
@@ -938,15 +954,28 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
         const char *e = getenv("QW_GEMM_SHAPE");
         shape = (e && (e[0] == 'a' || e[0] == 'b' || e[0] == 'r')) ? e[0] : 'b';
     }
-    int kid = (int8 && !widen ? K_GEMM_I8_STORE : K_GEMM_BF16_STORE) + d->epilogue;
+    const int qkn = d->epilogue == QW_LINEAR_QKNORM;
+    /* the fused q/k epilogue exists for shape b; other shapes store and
+     * run the separate norm + rope kernel afterwards */
+    const int qkn_after = qkn && shape != 'b';
+    int kid = (int8 && !widen ? K_GEMM_I8_STORE : K_GEMM_BF16_STORE) +
+              (qkn ? QW_LINEAR_STORE : d->epilogue);
     unsigned threads = 256, bm = 256, bn = 256;
     if (shape == 'b') {
         kid += K_GEMM_BF16_STORE_W8 - K_GEMM_BF16_STORE;
         threads = 512;
+        if (qkn) kid = int8 && !widen ? K_GEMM_I8_QKN_W8 : K_GEMM_BF16_QKN_W8;
     } else if (shape == 'r') {
         kid += K_GEMM_BF16_STORE_R - K_GEMM_BF16_STORE;
         bm = 128;
     }
+    a.norm_q = qkn ? (const uint16_t *)d->norm_q->ptr : NULL;
+    a.norm_k = qkn ? (const uint16_t *)d->norm_k->ptr : NULL;
+    a.rope_cos = qkn ? (const float *)d->rope_cos->ptr : NULL;
+    a.rope_sin = qkn ? (const float *)d->rope_sin->ptr : NULL;
+    a.rope_rows = qkn ? d->rope_rows : 1;
+    a.qk_cols = qkn ? d->cols / 3 * 2 : 0;
+    a.eps = qkn ? d->eps : 0.0f;
     a.tiles_m = (d->rows + bm - 1) / bm;
     a.tiles_n = (d->cols + bn - 1) / bn;
     const uint32_t tiles = a.tiles_m * a.tiles_n;
@@ -981,7 +1010,12 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
             grid = a.dp_tiles + R * s;
         }
     }
-    return launch(g, kid, dim3(grid), dim3(threads), a);
+    if (!launch(g, kid, dim3(grid), dim3(threads), a)) return 0;
+    if (qkn_after)
+        return qw_gpu_qk_norm_rope_bf16(g, d->out, d->rows, d->cols / 384, d->ldc, d->cols / 3,
+                                        d->norm_q, d->norm_k, d->rope_cos, d->rope_sin,
+                                        d->rope_rows, d->eps);
+    return 1;
 }
 
 static qw_linear_desc plain_linear(h3_gpu_tensor *out, const h3_gpu_tensor *in,

@@ -210,6 +210,15 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx1
             for (int j = 0; j < 4; j++) bias[2 * j] = lo_bf(bb[j]), bias[2 * j + 1] = hi_bf(bb[j]);
         }
     }
+    /* QW_EPI_QKNORM: this wave's 128 columns are one head (tiles start at
+     * multiples of 256); q or k heads get the norm weight of their kind */
+    const bool qk_head = EPI == QW_EPI_QKNORM && col0 < a.qk_cols;
+    float nw[8];
+    if (EPI == QW_EPI_QKNORM && qk_head) {
+        const u32x4 wn = *(const u32x4 *)((col0 < a.qk_cols / 2 ? a.norm_q : a.norm_k) + 8 * cc);
+#pragma unroll
+        for (int i = 0; i < 4; i++) nw[2 * i] = lo_bf(wn[i]), nw[2 * i + 1] = hi_bf(wn[i]);
+    }
     /* first/second 16-byte halves of the lane's 32 read-back bytes:
      * lanes 8-15 of a row start with the upper half, so one ds_read_b128
      * pass covers all 64 banks */
@@ -229,6 +238,9 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx1
             const floatx4 v0 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * swap);
             const floatx4 v1 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * (swap ^ 1));
             const uint32_t row = row0 + mi * 32 + lr;
+            /* a 16-lane row group is all in or all out (n % 8 == 0 for the
+             * columns; one row per group), so the QKNORM shuffles stay
+             * within active groups */
             if (!col_ok || row >= a.m) continue;
             float y[8];
 #pragma unroll
@@ -278,6 +290,29 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx1
                 y[j] = bf2f(f2bf(t + bias[j]));
             }
             u16 *dst = a.out + (size_t)row * a.ldc + col;
+            if (EPI == QW_EPI_QKNORM && qk_head) {
+                /* the 16 lanes of this row hold one head, 8 elements each
+                 * (lane cc: elements 8 cc..8 cc + 7), as qw_qk_norm_rope_bf16
+                 * holds it: the same sum order, shuffles and roundings */
+                float ss = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) ss = fmaf(y[j], y[j], ss);
+#pragma unroll
+                for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+                const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = bf2f(f2bf(y[j] * inv * nw[j]));
+                const size_t t = (size_t)(row % a.rope_rows) * 64 + 4 * cc;
+                const floatx4 rc = *(const floatx4 *)(a.rope_cos + t);
+                const floatx4 rs = *(const floatx4 *)(a.rope_sin + t);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float y0 = y[2 * i] * rc[i] - y[2 * i + 1] * rs[i];
+                    const float y1 = y[2 * i] * rs[i] + y[2 * i + 1] * rc[i];
+                    y[2 * i] = y0;
+                    y[2 * i + 1] = y1;
+                }
+            }
             if (EPI == QW_EPI_GELU) {
 #pragma unroll
                 for (int j = 0; j < 8; j++) y[j] = gelu_tanh_f(y[j]);
@@ -756,3 +791,5 @@ QW_GEMM_ENTRY(qw_gemm_bf16_gate_w8, QW_EPI_GATE, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_
 QW_GEMM_ENTRY(qw_gemm_i8_store_w8, QW_EPI_STORE, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
 QW_GEMM_ENTRY(qw_gemm_i8_gelu_w8, QW_EPI_GELU, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
 QW_GEMM_ENTRY(qw_gemm_i8_gate_w8, QW_EPI_GATE, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
+QW_GEMM_ENTRY(qw_gemm_bf16_qkn_w8, QW_EPI_QKNORM, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
+QW_GEMM_ENTRY(qw_gemm_i8_qkn_w8, QW_EPI_QKNORM, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)

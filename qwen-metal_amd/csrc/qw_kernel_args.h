@@ -12,7 +12,10 @@
 enum {
     QW_EPI_STORE = 0, /* store y */
     QW_EPI_GELU = 1,  /* store bf16(gelu_tanh(y)) */
-    QW_EPI_GATE = 2   /* out = bf16(out + y * gate[row_map[r]][n]) in place */
+    QW_EPI_GATE = 2,  /* out = bf16(out + y * gate[row_map[r]][n]) in place */
+    QW_EPI_QKNORM = 3 /* store y; columns below qk_cols (q then k heads of 128)
+                       * first get the per-head RMS norm and the RoPE rotation
+                       * of qw_qk_norm_rope_bf16, with its rounding points */
 };
 
 typedef struct {
@@ -38,6 +41,12 @@ typedef struct {
     uint32_t dp_tiles, split;
     float *sk_part;
     uint32_t *sk_flag;
+    /* QW_EPI_QKNORM: norm weights (k from column qk_cols / 2 on), RoPE
+     * tables [rope_rows, 64] (table row = row % rope_rows), epsilon */
+    const uint16_t *norm_q, *norm_k;
+    const float *rope_cos, *rope_sin;
+    uint32_t rope_rows, qk_cols;
+    float eps;
 } qw_gemm_args;
 
 typedef struct {

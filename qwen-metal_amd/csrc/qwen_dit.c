@@ -931,6 +931,35 @@ typedef struct {
     uint32_t base, rows;
 } qw_kv_cache;
 
+/* The fused q|k|v projection with the per-head RMS norm of q and k
+ * (h3_shaders.metal:4309-4329) and their RoPE (4864-4896) in its epilogue:
+ * one launch, the same result as the linear followed by
+ * qw_gpu_qk_norm_rope_bf16. */
+static int qkv_linear(qw_dit *d, const qw_layer *L, uint32_t M, const h3_gpu_tensor *rope_cos,
+                      const h3_gpu_tensor *rope_sin, uint32_t rope_rows) {
+    const uint32_t H = d->cfg.hidden;
+    qw_linear_desc desc;
+    memset(&desc, 0, sizeof(desc));
+    desc.out = d->ws_qkv;
+    desc.ldc = 3 * H;
+    desc.in = d->ws_mod;
+    desc.lda = H;
+    desc.weight = L->qkv.w;
+    desc.wscale = L->qkv.scales;
+    desc.bias = L->qkv.bias;
+    desc.rows = M;
+    desc.k = H;
+    desc.cols = 3 * H;
+    desc.epilogue = QW_LINEAR_QKNORM;
+    desc.norm_q = L->norm_q;
+    desc.norm_k = L->norm_k;
+    desc.rope_cos = rope_cos;
+    desc.rope_sin = rope_sin;
+    desc.rope_rows = rope_rows;
+    desc.eps = 1e-6f;
+    return qw_gpu_linear(d->gpu, &desc);
+}
+
 static int block_run(qw_dit *d, int li, h3_gpu_tensor *hidden, uint32_t batch, uint32_t rows,
                      uint32_t text_rows, const h3_gpu_tensor *modulation,
                      const h3_gpu_tensor *rope_cos, const h3_gpu_tensor *rope_sin,
@@ -947,9 +976,7 @@ static int block_run(qw_dit *d, int li, h3_gpu_tensor *hidden, uint32_t batch, u
     prof_begin(d);
     ok = qw_gpu_layer_norm_mod_shift_bf16(g, d->ws_mod, hidden, modulation, row_map, M, H, S, 0,
                                           sh ? 4 : -1, 1e-6f) &&
-         plain(d, &L->qkv, d->ws_qkv, d->ws_mod, M, QW_LINEAR_STORE) &&
-         qw_gpu_qk_norm_rope_bf16(g, d->ws_qkv, M, d->cfg.heads, 3 * H, H, L->norm_q, L->norm_k,
-                                  rope_cos, rope_sin, rows, 1e-6f);
+         qkv_linear(d, L, M, rope_cos, rope_sin, rows);
     prof_end(d, P_INPUT);
     if (!ok) return 0;
 

@@ -17,7 +17,7 @@ HSACO_PATH = os.path.join(LIB_DIR, "qwen_kernels.hsaco")
 F32, BF16, I8, U32 = 0, 1, 2, 3
 _NP = {F32: np.float32, BF16: np.uint16, I8: np.int8, U32: np.uint32}
 MLP_SWIGLU, MLP_GELU_TANH = 0, 1
-LINEAR_STORE, LINEAR_GELU, LINEAR_GATE = 0, 1, 2
+LINEAR_STORE, LINEAR_GELU, LINEAR_GATE, LINEAR_QKNORM = 0, 1, 2, 3
 
 vp = C.c_void_p
 u32 = C.c_uint32
@@ -61,7 +61,8 @@ class LinearDesc(C.Structure):
                 ("in_offset", sz), ("lda", u32), ("weight", vp), ("wscale", vp),
                 ("bias", vp), ("rows", u32), ("k", u32), ("cols", u32),
                 ("epilogue", C.c_int), ("modulation", vp), ("row_map", vp),
-                ("slots", u32), ("gate_slot", u32)]
+                ("slots", u32), ("gate_slot", u32), ("norm_q", vp), ("norm_k", vp),
+                ("rope_cos", vp), ("rope_sin", vp), ("rope_rows", u32), ("eps", C.c_float)]
 
 
 class AttentionDesc(C.Structure):
@@ -335,11 +336,14 @@ class Gpu:
     # ---- dispatch helpers (enqueue only) ----
     def linear(self, out, inp, weight, rows, k, cols, bias=None, wscale=None,
                epilogue=LINEAR_STORE, ldc=None, lda=None, out_offset=0, in_offset=0,
-               modulation=None, row_map=None, slots=0, gate_slot=0):
+               modulation=None, row_map=None, slots=0, gate_slot=0, qknorm=None):
+        """qknorm = (norm_q, norm_k, rope_cos, rope_sin, rope_rows, eps) with
+        epilogue LINEAR_QKNORM"""
+        nq, nk, rc, rs, rr, eps = qknorm if qknorm else (None, None, None, None, 0, 0.0)
+        h = lambda t: t.h if t is not None else None  # noqa: E731
         d = LinearDesc(out.h, out_offset, ldc or cols, inp.h, in_offset, lda or k, weight.h,
-                       wscale.h if wscale else None, bias.h if bias else None, rows, k, cols,
-                       epilogue, modulation.h if modulation else None,
-                       row_map.h if row_map else None, slots, gate_slot)
+                       h(wscale), h(bias), rows, k, cols, epilogue, h(modulation), h(row_map),
+                       slots, gate_slot, h(nq), h(nk), h(rc), h(rs), rr, eps)
         self.check(lib().qw_gpu_linear(self.h, C.byref(d)), "linear")
 
     def attention(self, out, q, k, v, batch, q_rows, kv_rows, heads, ldq, ldk, ldv, ldo,

@@ -226,6 +226,43 @@ def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
     assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
+@pytest.mark.parametrize("rows,int8,rope_rows", [(300, False, 300), (300, True, 150),
+                                                 (1000, True, 500), (4357, False, 4357)])
+def test_linear_qknorm_epilogue_bit_identical(gpu, qd, oracle, rows, int8, rope_rows):
+    """The fused q|k|v linear with the per-head RMS norm and RoPE of q and k
+    in its epilogue equals the linear followed by qw_gpu_qk_norm_rope_bf16,
+    bit for bit (same sums, same reduction order, same roundings): fused
+    int8 kernel, widen route, ragged rows, a RoPE table shorter than the
+    rows (batched sequences)."""
+    heads, k = 4, 512
+    n = 3 * heads * 128
+    x = synth(oracle, rows * k, 31)
+    w = synth(oracle, n * k, 32, 0.02)
+    b = synth(oracle, n, 33, 0.02)
+    nq, nk = synth(oracle, 128, 34, 0.1), synth(oracle, 128, 35, 0.1)
+    rng = np.random.default_rng(9)
+    ang = rng.uniform(-3, 3, (rope_rows, 64)).astype(np.float32)
+    cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    xt, bt, nqt, nkt, ct, st_ = (gpu.put(v) for v in (x, b, nq, nk, cos, sin))
+    if int8:
+        q, s = oracle.quantize_int8_rows(w, n, k)
+        wt, sc = gpu.put(q), gpu.put(s)
+    else:
+        wt, sc = gpu.put(w), None
+    fused, ref = gpu.new(rows * n, qd.BF16), gpu.new(rows * n, qd.BF16)
+    gpu.linear(fused, xt, wt, rows, k, n, bias=bt, wscale=sc, epilogue=qd.LINEAR_QKNORM,
+               qknorm=(nqt, nkt, ct, st_, rope_rows, 1e-6))
+    gpu.linear(ref, xt, wt, rows, k, n, bias=bt, wscale=sc)
+    gpu.check(qd.lib().qw_gpu_qk_norm_rope_bf16(gpu.h, ref.h, rows, heads, n, n // 3, nqt.h,
+                                                 nkt.h, ct.h, st_.h, rope_rows, 1e-6), "qk")
+    gpu.submit()
+    assert np.array_equal(fused.read(), ref.read())
+    bad = gpu.new(rows * 1024, qd.BF16)
+    with pytest.raises(RuntimeError, match="heads of 128"):
+        gpu.linear(bad, xt, gpu.new(1024 * k, qd.BF16), rows, k, 1024,
+                   epilogue=qd.LINEAR_QKNORM, qknorm=(nqt, nkt, ct, st_, rope_rows, 1e-6))
+
+
 def test_linear_strided_views(gpu, qd, oracle):
     """Offsets/strides as the DiT uses them (rows written into a joint
     buffer at a row offset, input read from a wider buffer)."""
