@@ -233,6 +233,54 @@ def denoise_512(qd, gpu):
     return res
 
 
+def ti2i_1024(qd, gpu, dit):
+    """ti2i at the workload's geometry (the step's int8 model): 256 text
+    rows, a 1024x1024 condition image (4096 rows), 64 text rows and the
+    1024x1024 target (4096 rows); one forward through qw_dit_forward_ti2i
+    as a full pass (cache cleared) against one with the conditioning K/V
+    cached (target rows only), the reference's cross-step cache
+    (qwen_dit.m:1694-1699)."""
+    import ctypes as C
+    L = qd.lib()
+
+    class Seg(C.Structure):
+        _fields_ = [("rows", C.c_uint32), ("is_image", C.c_int), ("src_offset", C.c_uint32)]
+    segs = (Seg * 4)(Seg(256, 0, 0), Seg(4096, 1, 0), Seg(64, 0, 256), Seg(4096, 1, 4096))
+    rows = 256 + 4096 + 64 + 4096
+    text = gpu.new(320 * CFG["text_dim"], qd.BF16)
+    lat = gpu.new(8192 * CFG["z_dim"], qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, text.h, 0, text.n, SEED, 840, 1.0, 0.0), "fill")
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, lat.h, 0, lat.n, SEED, 841, 1.0, 0.0), "fill")
+    cos = np.empty((rows, 64), np.float32)
+    sin = np.empty((rows, 64), np.float32)
+    L.qw_pipe_rope_tables_host(rows - 4096, 64, 64, cos.ctypes.data, sin.ctypes.data)
+    ct, st = gpu.put(cos), gpu.put(sin)
+    out = gpu.new(rows * CFG["z_dim"], qd.BF16)
+    err = C.create_string_buffer(1024)
+
+    def run(sigma):
+        if not L.qw_dit_forward_ti2i(dit.h, text.h, lat.h, segs, 4, 0, ct.h, st.h, sigma, out.h,
+                                     err, 1024):
+            raise RuntimeError(err.value.decode())
+    full, cached = [], []
+    for _ in range(2):
+        L.qw_dit_ti2i_cache_clear(dit.h)
+        gpu.submit()
+        t = time.time()
+        run(0.9)
+        gpu.submit()
+        full.append((time.time() - t) * 1e3)
+        t = time.time()
+        run(0.8)
+        gpu.submit()
+        cached.append((time.time() - t) * 1e3)
+    L.qw_dit_ti2i_cache_clear(dit.h)
+    for x in (text, lat, ct, st, out):
+        x.free()
+    return {"rows": rows, "target_rows": 4096, "full_pass_ms": min(full),
+            "cached_step_ms": min(cached), "speedup": min(full) / min(cached)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -302,6 +350,7 @@ def main():
                               "int8 weight widened by qw_widen_i8_bf16, scale in the epilogue)",
                     "flop_per_launch": fl, "ms_per_launch": up["gemm_ms"]}
     den = None if args.no_breakdown or args.no_denoise else denoise_512(qd, gpu)
+    ti2i = None if args.no_breakdown or args.no_denoise else ti2i_1024(qd, gpu, dit)
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": "DiT ms/step @1024^2 (4352 tok, CFG b=2); linear+SDPA TFLOP/s & % MFMA peak",
@@ -318,6 +367,7 @@ def main():
         "flop_per_step": {"linear": lin, "sdpa": sdpa, "other": extra},
         "breakdown": brk,
         "denoise_512_8step": den,
+        "ti2i_1024_one_condition": ti2i,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "wall_ms_per_step": wall_ms / args.steps,
