@@ -358,11 +358,17 @@ struct PipeCtx {
 /* One K-slice: multiply the stage `cur` while slice k_next streams into the
  * stage `nxt`. The two stages are distinct (restrict) so the scheduler may
  * interleave the LDS fragment reads of one with the direct loads into the
- * other; sched_group_barrier then lays out the pipeline: fragment reads of
- * sub-step s + 1, the slice loads and the int8 LDS writes between MFMAs. */
-template <int INT8, int MI, int NI, int A_BYTES, int A_DL, int W_DL, int WLD, int WROWS>
+ * other. The last sub-step's MFMAs are held back: they run at the start of
+ * the next slice (PREV), after the barrier, under the LDS reads of that
+ * slice's first fragments, so the matrix pipe does not drain at each
+ * barrier. pa / pw carry those fragments from one slice to the next.
+ * sched_group_barrier lays out the pipeline: fragment reads of sub-step
+ * s + 1, the slice loads and the int8 LDS writes between MFMAs. */
+template <int INT8, int MI, int NI, int A_BYTES, int A_DL, int W_DL, int WLD, int WROWS,
+          bool PREV>
 __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &c,
-                                                floatx16 (&acc)[NI][MI],
+                                                floatx16 (&acc)[NI][MI], bf16x8 (&pa)[MI],
+                                                bf16x8 (&pw)[NI],
                                                 const unsigned char *__restrict__ cur,
                                                 unsigned char *__restrict__ nxt,
                                                 uint32_t k_next) {
@@ -384,7 +390,6 @@ __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &
             rw[j] = __builtin_bit_cast(
                 u32x4, __builtin_amdgcn_raw_buffer_load_b128(c.w_rsrc, c.w_off[j] + k_next, 0, 0));
     }
-    /* MFMAs of this slice, fragments double-buffered across sub-steps */
     const unsigned char *As = cur, *Ws = cur + A_BYTES;
 #define QW_FR(row, ks) ((row) * 128u + (((2 * (ks) + c.h) ^ c.swz) << 4))
     bf16x8 af[2][MI], bw[2][NI];
@@ -392,17 +397,23 @@ __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &
     for (int i = 0; i < MI; i++) af[0][i] = *(const bf16x8 *)(As + QW_FR(c.a_row0 + 32 * i, 0));
 #pragma unroll
     for (int i = 0; i < NI; i++) bw[0][i] = *(const bf16x8 *)(Ws + QW_FR(c.w_row0 + 32 * i, 0));
+    if (PREV) { /* the previous slice's last sub-step */
 #pragma unroll
-    for (uint32_t ks = 0; ks < 4; ks++) {
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int mi = 0; mi < MI; mi++)
+                acc[ni][mi] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(pw[ni], pa[mi], acc[ni][mi], 0, 0, 0);
+    }
+#pragma unroll
+    for (uint32_t ks = 0; ks < 3; ks++) {
         const int b = ks & 1;
-        if (ks + 1 < 4) {
 #pragma unroll
-            for (int i = 0; i < MI; i++)
-                af[b ^ 1][i] = *(const bf16x8 *)(As + QW_FR(c.a_row0 + 32 * i, ks + 1));
+        for (int i = 0; i < MI; i++)
+            af[b ^ 1][i] = *(const bf16x8 *)(As + QW_FR(c.a_row0 + 32 * i, ks + 1));
 #pragma unroll
-            for (int i = 0; i < NI; i++)
-                bw[b ^ 1][i] = *(const bf16x8 *)(Ws + QW_FR(c.w_row0 + 32 * i, ks + 1));
-        }
+        for (int i = 0; i < NI; i++)
+            bw[b ^ 1][i] = *(const bf16x8 *)(Ws + QW_FR(c.w_row0 + 32 * i, ks + 1));
 #pragma unroll
         for (int ni = 0; ni < NI; ni++)
 #pragma unroll
@@ -411,6 +422,10 @@ __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &
                                                                       acc[ni][mi], 0, 0, 0);
     }
 #undef QW_FR
+#pragma unroll
+    for (int i = 0; i < MI; i++) pa[i] = af[1][i];
+#pragma unroll
+    for (int i = 0; i < NI; i++) pw[i] = bw[1][i];
     if (INT8) {
         unsigned char *Wn = nxt + A_BYTES;
 #pragma unroll
@@ -426,25 +441,25 @@ __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &
     constexpr int NV = A_DL + W_DL + (INT8 ? WLD : 0);
     constexpr int NW = INT8 ? 2 * WLD : 0;
     static_assert(NV <= NMF && NW <= NMF && NRD <= NMF, "pipeline pattern");
-    __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0); /* fragments of step 0 */
+    if (PREV) {
 #pragma unroll
-    for (int i = 0; i < NMF; i++) { /* step 0: slice loads + fragments of step 1 */
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (i < NV) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-#pragma unroll
-    for (int st = 1; st < 3; st++)
-#pragma unroll
-        for (int i = 0; i < NMF; i++) { /* steps 1, 2: fragments of the next step */
+        for (int i = 0; i < NMF; i++) { /* held-back MFMAs: slice loads + fragments of step 0 */
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i < NV) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-#pragma unroll
-    for (int i = 0; i < NMF; i++) { /* step 3: int8 W writes of slice k_next */
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (i < NW) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    } else {
+        __builtin_amdgcn_sched_group_barrier(0x020, NV, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
     }
+#pragma unroll
+    for (int st = 0; st < 3; st++)
+#pragma unroll
+        for (int i = 0; i < NMF; i++) { /* steps 0-2: fragments of the next step */
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (st == 2 && i < NW) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+        }
 }
 
 /* Sums of tile (tm, tn) over k-steps [kb, ke) (64 k each) into acc; the
@@ -623,14 +638,28 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
         }
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): direct loads landed */
         __syncthreads();
-        for (uint32_t kt = kb; kt < KT; kt++) {
-            const uint32_t odd = (kt - kb) & 1;
-            const uint32_t nk = (kt + 1 < KT ? kt + 1 : kt) * GBK;
-            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS>(
-                c, acc, odd ? lds_b : lds, odd ? lds : lds_b, QW_K(nk));
+        bf16x8 pa[MI], pw[NI]; /* last sub-step's fragments, multiplied one slice late */
+        {
+            const uint32_t nk = (kb + 1 < KT ? kb + 1 : kb) * GBK;
+            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, false>(
+                c, acc, pa, pw, lds, lds_b, QW_K(nk));
             __builtin_amdgcn_s_waitcnt(0x0F70);
             __syncthreads();
         }
+        for (uint32_t kt = kb + 1; kt < KT; kt++) {
+            const uint32_t odd = (kt - kb) & 1;
+            const uint32_t nk = (kt + 1 < KT ? kt + 1 : kt) * GBK;
+            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                c, acc, pa, pw, odd ? lds_b : lds, odd ? lds : lds_b, QW_K(nk));
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+        }
+#pragma unroll
+        for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+            for (int mi = 0; mi < MI; mi++)
+                acc[ni][mi] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(pw[ni], pa[mi], acc[ni][mi], 0, 0, 0);
     } else if (PF == 1) {
         QW_LOAD(0, 0);
         store_lds(ra[0], rw[0], 0);
