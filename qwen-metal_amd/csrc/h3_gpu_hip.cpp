@@ -815,8 +815,9 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
 static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps) {
     static int mode = -1;
     if (mode < 0) {
+        /* unset, empty or "auto": automatic; 0 or 1: off; N: N pieces */
         const char *e = getenv("QW_GEMM_SPLIT");
-        mode = e ? atoi(e) : 9999; /* 9999: automatic */
+        mode = !e || !e[0] || !strcmp(e, "auto") ? 9999 : atoi(e);
         if (mode < 0) mode = 0;
     }
     if (mode <= 1) return 1;
