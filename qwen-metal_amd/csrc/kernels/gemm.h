@@ -373,22 +373,23 @@ __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &
                                                 unsigned char *__restrict__ nxt,
                                                 uint32_t k_next) {
     typedef __attribute__((address_space(3))) void lds_void;
-    /* slice k_next: A (and bf16 W) straight into LDS */
+    /* slice k_next: A (and bf16 W) straight into LDS; the k advance rides
+     * in the scalar offset, so the lane offsets need no per-slice VALU */
 #pragma unroll
     for (int j = 0; j < A_DL; j++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(c.a_rsrc, (lds_void *)(nxt + c.a_dst0 + j * 1024),
-                                                 16, c.a_dvoff[j] + k_next * 2, 0, 0, 0);
+                                                 16, c.a_dvoff[j], k_next * 2, 0, 0);
 #pragma unroll
     for (int j = 0; j < W_DL; j++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(c.w_rsrc,
                                                  (lds_void *)(nxt + A_BYTES + c.w_dst0 + j * 1024),
-                                                 16, c.w_dvoff[j] + k_next * 2, 0, 0, 0);
+                                                 16, c.w_dvoff[j], k_next * 2, 0, 0);
     u32x4 rw[WLD];
     if (INT8) {
 #pragma unroll
         for (int j = 0; j < WLD; j++)
             rw[j] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(c.w_rsrc, c.w_off[j] + k_next, 0, 0));
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(c.w_rsrc, c.w_off[j], k_next, 0));
     }
     const unsigned char *As = cur, *Ws = cur + A_BYTES;
 #define QW_FR(row, ks) ((row) * 128u + (((2 * (ks) + c.h) ^ c.swz) << 4))
@@ -646,11 +647,22 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
             __builtin_amdgcn_s_waitcnt(0x0F70);
             __syncthreads();
         }
-        for (uint32_t kt = kb + 1; kt < KT; kt++) {
-            const uint32_t odd = (kt - kb) & 1;
-            const uint32_t nk = (kt + 1 < KT ? kt + 1 : kt) * GBK;
+        /* two slices per trip, so each one's stages are fixed at compile
+         * time and their LDS bases fold into the instructions' offsets */
+        uint32_t kt = kb + 1;
+        for (; kt + 1 < KT; kt += 2) {
             gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
-                c, acc, pa, pw, odd ? lds_b : lds, odd ? lds : lds_b, QW_K(nk));
+                c, acc, pa, pw, lds_b, lds, QW_K((kt + 1) * GBK));
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                c, acc, pa, pw, lds, lds_b, QW_K((kt + 2 < KT ? kt + 2 : kt + 1) * GBK));
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+        }
+        if (kt < KT) { /* the last slice, from stage lds_b */
+            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                c, acc, pa, pw, lds_b, lds, QW_K(kt * GBK));
             __builtin_amdgcn_s_waitcnt(0x0F70);
             __syncthreads();
         }
