@@ -128,7 +128,7 @@ def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, calibrated against
     a copy kernel of known size), or None when it has not been measured."""
-    p = os.path.join(ROOT, "profiles", "gemm_up_bf16_gelu_w8_traffic.md")
+    p = os.path.join(ROOT, "profiles", "gemm_up_bf16_gelu_d_traffic.md")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -346,7 +346,7 @@ def main():
         roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
                     "traffic": measured_traffic(),
-                    "kernel": "qw_gemm_bf16_gelu_w8 (up-projection, M=8704 K=3072 N=12288, "
+                    "kernel": "qw_gemm_bf16_gelu_d (up-projection, M=8704 K=3072 N=12288, "
                               "int8 weight widened by qw_widen_i8_bf16, scale in the epilogue)",
                     "flop_per_launch": fl, "ms_per_launch": up["gemm_ms"]}
     den = None if args.no_breakdown or args.no_denoise else denoise_512(qd, gpu)

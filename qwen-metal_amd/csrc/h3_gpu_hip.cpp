@@ -29,6 +29,7 @@ enum {
     K_GEMM_BF16_STORE_W8, K_GEMM_BF16_GELU_W8, K_GEMM_BF16_GATE_W8,
     K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_GEMM_BF16_QKN_W8,
     K_GEMM_I8_QKN_W8,
+    K_GEMM_BF16_STORE_D, K_GEMM_BF16_GELU_D, K_GEMM_BF16_GATE_D, K_GEMM_BF16_QKN_D,
     K_GEMM_BF16_STORE_R, K_GEMM_BF16_GELU_R, K_GEMM_BF16_GATE_R,
     K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA, K_COUNT
 };
@@ -42,6 +43,7 @@ static const char *k_names[K_COUNT] = {
     "qw_gemm_bf16_store_w8", "qw_gemm_bf16_gelu_w8", "qw_gemm_bf16_gate_w8",
     "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8",
     "qw_gemm_bf16_qkn_w8", "qw_gemm_i8_qkn_w8",
+    "qw_gemm_bf16_store_d", "qw_gemm_bf16_gelu_d", "qw_gemm_bf16_gate_d", "qw_gemm_bf16_qkn_d",
     "qw_gemm_bf16_store_r", "qw_gemm_bf16_gelu_r", "qw_gemm_bf16_gate_r",
     "qw_gemm_i8_store_r", "qw_gemm_i8_gelu_r", "qw_gemm_i8_gate_r", "qw_widen_i8_bf16",
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16"};
@@ -947,18 +949,20 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
         a.a_bytes = (uint32_t)ab;
         a.w_bytes = (uint32_t)wb;
     }
-    /* kernel family: QW_GEMM_SHAPE = b (default: 256 x 256, 8 waves, two
-     * per SIMD), a (256 x 256, 4 waves) or r (128 x 256, 4 waves, two
-     * workgroups per CU) */
-    static char shape = 0;
-    if (!shape) {
+    /* kernel family: QW_GEMM_SHAPE = b (256 x 256, 8 waves, two
+     * per SIMD), a (256 x 256, 4 waves), r (128 x 256, 4 waves, two
+     * workgroups per CU) or d (default: b with 16x16x32 MFMAs, bf16 weights;
+     * in-loop int8 widening runs b's kernels) */
+    static char shape_env = 0;
+    if (!shape_env) {
         const char *e = getenv("QW_GEMM_SHAPE");
-        shape = (e && (e[0] == 'a' || e[0] == 'b' || e[0] == 'r')) ? e[0] : 'b';
+        shape_env = (e && e[0] && strchr("abdr", e[0])) ? e[0] : 'd';
     }
+    const char shape = shape_env == 'd' && int8 && !widen ? 'b' : shape_env;
     const int qkn = d->epilogue == QW_LINEAR_QKNORM;
-    /* the fused q/k epilogue exists for shape b; other shapes store and
+    /* the fused q/k epilogue exists for shapes b and d; a and r store and
      * run the separate norm + rope kernel afterwards */
-    const int qkn_after = qkn && shape != 'b';
+    const int qkn_after = qkn && (shape == 'a' || shape == 'r');
     int kid = (int8 && !widen ? K_GEMM_I8_STORE : K_GEMM_BF16_STORE) +
               (qkn ? QW_LINEAR_STORE : d->epilogue);
     unsigned threads = 256, bm = 256, bn = 256;
@@ -966,6 +970,10 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
         kid += K_GEMM_BF16_STORE_W8 - K_GEMM_BF16_STORE;
         threads = 512;
         if (qkn) kid = int8 && !widen ? K_GEMM_I8_QKN_W8 : K_GEMM_BF16_QKN_W8;
+    } else if (shape == 'd') { /* b's geometry with 16x16x32 MFMAs */
+        kid += K_GEMM_BF16_STORE_D - K_GEMM_BF16_STORE;
+        if (qkn) kid = K_GEMM_BF16_QKN_D;
+        threads = 512;
     } else if (shape == 'r') {
         kid += K_GEMM_BF16_STORE_R - K_GEMM_BF16_STORE;
         bm = 128;

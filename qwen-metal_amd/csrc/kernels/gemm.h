@@ -2,7 +2,7 @@
  *   out[m, n] = epilogue( sum_k A[m, k] * W[n, k] )
  * A bf16 row-major (row stride lda), W in the checkpoint's native [out, in]
  * layout (bf16, or int8 with one fp32 scale per output row), fp32
- * accumulation in v_mfma_f32_32x32x16_bf16.
+ * accumulation in v_mfma_f32_32x32x16_bf16 (or 16x16x32, shape D).
  *
  * Tiling (template): a workgroup of WM x WN waves computes a BM x BN tile,
  * BM = WM * MI * 32, BN = WN * NI * 32, each wave an (MI*32) x (NI*32) block
@@ -11,7 +11,9 @@
  *      accumulators per lane);
  *   B: 4 x 2 waves of 2 x 4 blocks (256 x 256, two waves per SIMD, 128
  *      accumulators each: one wave's MFMAs cover the other's LDS/global
- *      latency).
+ *      latency);
+ *   D: B's geometry with each 32 x 32 block computed as four 16 x 16 blocks
+ *      of v_mfma_f32_16x16x32_bf16 (the runtime's default for bf16 weights).
  * A and W tiles are staged through LDS, double-buffered (2 x 64 KB at
  * 256 x 256), with the next K-slice's global loads in flight while the
  * current one is multiplied; within a K-slice the operand fragments of
@@ -174,7 +176,7 @@ __device__ __forceinline__ void gemm_epilogue(const qw_gemm_args &a, floatx16 (&
  * instead of 16-byte pieces, and the residual/gate reads of the GATE
  * epilogue are coalesced the same way. A lane keeps the same 8 columns for
  * every row, so it loads their scale and bias once. */
-template <int EPI, int INT8, int MI, int NI>
+template <int EPI, int INT8, int MI, int NI, int MF = 32>
 __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx16 (&acc)[NI][MI],
                                                   float *region, uint32_t row0, uint32_t col0,
                                                   uint32_t h, uint32_t i32, uint32_t lane,
@@ -225,13 +227,28 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx1
     const uint32_t swap = (cc >> 3) & 1;
 #pragma unroll
     for (int mi = 0; mi < MI; mi++) {
+        if constexpr (MF == 16) { /* quarter 2p + q: rows 16 q + l % 16, cols 16 p + 4 (l / 16) */
 #pragma unroll
-        for (int ni = 0; ni < NI; ni++)
+            for (int ni = 0; ni < NI; ni++)
 #pragma unroll
-            for (int g = 0; g < 4; g++)
-                *(floatx4 *)(region + i32 * LDF + ni * 32 + 8 * g + 4 * h) =
-                    floatx4{acc[ni][mi][4 * g], acc[ni][mi][4 * g + 1], acc[ni][mi][4 * g + 2],
-                            acc[ni][mi][4 * g + 3]};
+                for (int p = 0; p < 2; p++)
+#pragma unroll
+                    for (int q = 0; q < 2; q++) {
+                        const int k = 2 * p + q;
+                        *(floatx4 *)(region + (16 * q + (lane & 15)) * LDF + ni * 32 + 16 * p +
+                                     4 * (lane >> 4)) =
+                            floatx4{acc[ni][mi][4 * k], acc[ni][mi][4 * k + 1],
+                                    acc[ni][mi][4 * k + 2], acc[ni][mi][4 * k + 3]};
+                    }
+        } else {
+#pragma unroll
+            for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    *(floatx4 *)(region + i32 * LDF + ni * 32 + 8 * g + 4 * h) =
+                        floatx4{acc[ni][mi][4 * g], acc[ni][mi][4 * g + 1], acc[ni][mi][4 * g + 2],
+                                acc[ni][mi][4 * g + 3]};
+        }
 #pragma unroll
         for (int p = 0; p < 8; p++) {
             const uint32_t lr = 4 * p + rr;
@@ -463,10 +480,126 @@ __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &
         }
 }
 
+/* Instructions of one kind placed after MFMA i of n: one each after the
+ * first `count` MFMAs, or spread evenly when there are more than MFMAs */
+__device__ constexpr int sched_share(int count, int n, int i) {
+    return count <= n ? (i < count ? 1 : 0) : count * (i + 1) / n - count * i / n;
+}
+
+/* 16 x 16 block q (0..3) of a 32 x 32 accumulator's registers (elements
+ * 4q..4q+3): the 16x16x32 MFMA path keeps the same accumulator arrays. */
+__device__ __forceinline__ void mfma16_into(floatx16 &acc, int q, bf16x8 a, bf16x8 b) {
+    floatx4 c4 = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+    c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c4, 0, 0, 0);
+    acc[4 * q] = c4[0];
+    acc[4 * q + 1] = c4[1];
+    acc[4 * q + 2] = c4[2];
+    acc[4 * q + 3] = c4[3];
+}
+
+/* gemm_pipe_slice with v_mfma_f32_16x16x32_bf16: two sub-steps of 32 k,
+ * 16-row fragments (lane l: row l % 16, k chunk 4 ks + l / 16), block
+ * (nb, mb) of C^T in quarter 2 (nb % 2) + mb % 2 of acc[nb / 2][mb / 2];
+ * the second sub-step is held back to the start of the next slice (PREV). */
+template <int INT8, int MI, int NI, int A_BYTES, int A_DL, int W_DL, int WLD, int WROWS,
+          bool PREV>
+__device__ __forceinline__ void gemm_pipe_slice16(const PipeCtx<A_DL, W_DL, WLD> &c,
+                                                  floatx16 (&acc)[NI][MI], bf16x8 (&pa)[2 * MI],
+                                                  bf16x8 (&pw)[2 * NI],
+                                                  const unsigned char *__restrict__ cur,
+                                                  unsigned char *__restrict__ nxt,
+                                                  uint32_t k_next) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    constexpr int MB = 2 * MI, NB = 2 * NI;
+#pragma unroll
+    for (int j = 0; j < A_DL; j++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.a_rsrc, (lds_void *)(nxt + c.a_dst0 + j * 1024),
+                                                 16, c.a_dvoff[j], k_next * 2, 0, 0);
+#pragma unroll
+    for (int j = 0; j < W_DL; j++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(c.w_rsrc,
+                                                 (lds_void *)(nxt + A_BYTES + c.w_dst0 + j * 1024),
+                                                 16, c.w_dvoff[j], k_next * 2, 0, 0);
+    u32x4 rw[WLD];
+    if (INT8) {
+#pragma unroll
+        for (int j = 0; j < WLD; j++)
+            rw[j] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(c.w_rsrc, c.w_off[j], k_next, 0));
+    }
+    const unsigned char *As = cur, *Ws = cur + A_BYTES;
+#define QW_FR16(row, ks) ((row) * 128u + (((4 * (ks) + c.h) ^ c.swz) << 4))
+    bf16x8 af[MB], bw[NB], af1[MB], bw1[NB];
+#pragma unroll
+    for (int i = 0; i < MB; i++) af[i] = *(const bf16x8 *)(As + QW_FR16(c.a_row0 + 16 * i, 0));
+#pragma unroll
+    for (int i = 0; i < NB; i++) bw[i] = *(const bf16x8 *)(Ws + QW_FR16(c.w_row0 + 16 * i, 0));
+    if (PREV) {
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+                mfma16_into(acc[nb >> 1][mb >> 1], 2 * (nb & 1) + (mb & 1), pw[nb], pa[mb]);
+    }
+#pragma unroll
+    for (int i = 0; i < MB; i++) af1[i] = *(const bf16x8 *)(As + QW_FR16(c.a_row0 + 16 * i, 1));
+#pragma unroll
+    for (int i = 0; i < NB; i++) bw1[i] = *(const bf16x8 *)(Ws + QW_FR16(c.w_row0 + 16 * i, 1));
+#undef QW_FR16
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+            mfma16_into(acc[nb >> 1][mb >> 1], 2 * (nb & 1) + (mb & 1), bw[nb], af[mb]);
+#pragma unroll
+    for (int i = 0; i < MB; i++) pa[i] = af1[i];
+#pragma unroll
+    for (int i = 0; i < NB; i++) pw[i] = bw1[i];
+    if (INT8) {
+        unsigned char *Wn = nxt + A_BYTES;
+#pragma unroll
+        for (int j = 0; j < WLD; j++) {
+            u32x4 lo, hi;
+            i8x16_to_bf16(rw[j], lo, hi);
+            const uint32_t r = c.wr + WROWS * j;
+            *(u32x4 *)(Wn + g_swz(r, 2 * c.wc)) = lo;
+            *(u32x4 *)(Wn + g_swz(r, 2 * c.wc + 1)) = hi;
+        }
+    }
+    constexpr int NMF = MB * NB, NRD = MB + NB;
+    constexpr int NV = A_DL + W_DL + (INT8 ? WLD : 0);
+    constexpr int NW = INT8 ? 2 * WLD : 0;
+    if (PREV) {
+#pragma unroll
+        for (int i = 0; i < NMF; i++) { /* held-back MFMAs: slice loads + fragments of step 0 */
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+            for (int q = 0; q < sched_share(NV, NMF, i); q++)
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+#pragma unroll
+            for (int q = 0; q < sched_share(NRD, NMF, i); q++)
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+    } else {
+        __builtin_amdgcn_sched_group_barrier(0x020, NV, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < NMF; i++) { /* step 0: fragments of step 1, int8 W writes */
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+#pragma unroll
+        for (int q = 0; q < sched_share(NRD, NMF, i); q++)
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+#pragma unroll
+        for (int q = 0; q < sched_share(NW, NMF, i); q++)
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+    }
+}
+
 /* Sums of tile (tm, tn) over k-steps [kb, ke) (64 k each) into acc; the
  * PF == 1, 2 pipelines take the whole k range only. Ends with the LDS
  * stages free (after a barrier). */
-template <int INT8, int WM, int WN, int MI, int NI, int PF, int FDB>
+template <int INT8, int WM, int WN, int MI, int NI, int PF, int FDB, int MF = 32>
 __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned char *lds,
                                               unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                               uint32_t kb, uint32_t ke,
@@ -611,10 +744,10 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
         }
 #pragma unroll
         for (int j = 0; j < WLD; j++) c.w_off[j] = w_off[j];
-        c.a_row0 = a_row0;
-        c.w_row0 = w_row0;
-        c.swz = swz;
-        c.h = h;
+        c.a_row0 = MF == 16 ? wm * (MI * 32) + (lane & 15) : a_row0;
+        c.w_row0 = MF == 16 ? wn * (NI * 32) + (lane & 15) : w_row0;
+        c.swz = MF == 16 ? ((lane & 15) >> 1) & 7u : swz;
+        c.h = MF == 16 ? lane >> 4 : h;
         c.a_dst0 = wave * (S::BM / NWAVE) * 128;
         c.w_dst0 = wave * (S::BN / NWAVE) * 128;
         c.wr = wr;
@@ -639,39 +772,74 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
         }
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): direct loads landed */
         __syncthreads();
-        bf16x8 pa[MI], pw[NI]; /* last sub-step's fragments, multiplied one slice late */
-        {
-            const uint32_t nk = (kb + 1 < KT ? kb + 1 : kb) * GBK;
-            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, false>(
-                c, acc, pa, pw, lds, lds_b, QW_K(nk));
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-            __syncthreads();
+        if constexpr (MF == 16) {
+            bf16x8 pa[2 * MI], pw[2 * NI]; /* last sub-step's fragments, multiplied one slice late */
+            {
+                const uint32_t nk = (kb + 1 < KT ? kb + 1 : kb) * GBK;
+                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, false>(
+                    c, acc, pa, pw, lds, lds_b, QW_K(nk));
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+            }
+            /* two slices per trip, so each one's stages are fixed at compile
+             * time and their LDS bases fold into the instructions' offsets */
+            uint32_t kt = kb + 1;
+            for (; kt + 1 < KT; kt += 2) {
+                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                    c, acc, pa, pw, lds_b, lds, QW_K((kt + 1) * GBK));
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                    c, acc, pa, pw, lds, lds_b, QW_K((kt + 2 < KT ? kt + 2 : kt + 1) * GBK));
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+            }
+            if (kt < KT) { /* the last slice, from stage lds_b */
+                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                    c, acc, pa, pw, lds_b, lds, QW_K(kt * GBK));
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+            }
+    #pragma unroll
+            for (int nb = 0; nb < 2 * NI; nb++)
+    #pragma unroll
+                for (int mb = 0; mb < 2 * MI; mb++)
+                    mfma16_into(acc[nb >> 1][mb >> 1], 2 * (nb & 1) + (mb & 1), pw[nb], pa[mb]);
+        } else {
+            bf16x8 pa[MI], pw[NI]; /* last sub-step's fragments, multiplied one slice late */
+            {
+                const uint32_t nk = (kb + 1 < KT ? kb + 1 : kb) * GBK;
+                gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, false>(
+                    c, acc, pa, pw, lds, lds_b, QW_K(nk));
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+            }
+            /* two slices per trip, so each one's stages are fixed at compile
+             * time and their LDS bases fold into the instructions' offsets */
+            uint32_t kt = kb + 1;
+            for (; kt + 1 < KT; kt += 2) {
+                gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                    c, acc, pa, pw, lds_b, lds, QW_K((kt + 1) * GBK));
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+                gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                    c, acc, pa, pw, lds, lds_b, QW_K((kt + 2 < KT ? kt + 2 : kt + 1) * GBK));
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+            }
+            if (kt < KT) { /* the last slice, from stage lds_b */
+                gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                    c, acc, pa, pw, lds_b, lds, QW_K(kt * GBK));
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+            }
+    #pragma unroll
+            for (int ni = 0; ni < NI; ni++)
+    #pragma unroll
+                for (int mi = 0; mi < MI; mi++)
+                    acc[ni][mi] =
+                        __builtin_amdgcn_mfma_f32_32x32x16_bf16(pw[ni], pa[mi], acc[ni][mi], 0, 0, 0);
         }
-        /* two slices per trip, so each one's stages are fixed at compile
-         * time and their LDS bases fold into the instructions' offsets */
-        uint32_t kt = kb + 1;
-        for (; kt + 1 < KT; kt += 2) {
-            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
-                c, acc, pa, pw, lds_b, lds, QW_K((kt + 1) * GBK));
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-            __syncthreads();
-            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
-                c, acc, pa, pw, lds, lds_b, QW_K((kt + 2 < KT ? kt + 2 : kt + 1) * GBK));
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-            __syncthreads();
-        }
-        if (kt < KT) { /* the last slice, from stage lds_b */
-            gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
-                c, acc, pa, pw, lds_b, lds, QW_K(kt * GBK));
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-            __syncthreads();
-        }
-#pragma unroll
-        for (int ni = 0; ni < NI; ni++)
-#pragma unroll
-            for (int mi = 0; mi < MI; mi++)
-                acc[ni][mi] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(pw[ni], pa[mi], acc[ni][mi], 0, 0, 0);
     } else if (PF == 1) {
         QW_LOAD(0, 0);
         store_lds(ra[0], rw[0], 0);
@@ -710,7 +878,7 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
 /* Epilogue of a finished tile (bf16 output plus the EPI op), or with pst the
  * fp32 sums of one piece of a split tile, or with pld the sum of all its
  * pieces followed by the epilogue */
-template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF>
+template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int MF = 32>
 __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char *lds,
                                             unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                             floatx16 (&acc)[NI][MI], float *pst = nullptr,
@@ -732,7 +900,7 @@ __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char
         /* split-tile partials: row-major 256 x 256 fp32 */
         static_assert(S::BN == 256 && S::BM * S::BN <= QW_SPLIT_PART, "partial tile size");
         const uint32_t poff = wm * (MI * 32) * 256 + wn * (NI * 32);
-        gemm_epilogue_lds<EPI, INT8, MI, NI>(a, acc, region, row0, col0, h, i32, lane,
+        gemm_epilogue_lds<EPI, INT8, MI, NI, MF>(a, acc, region, row0, col0, h, i32, lane,
                                              pst ? pst + poff : nullptr, pld ? pld + poff : nullptr,
                                              npart, own);
         return;
@@ -741,7 +909,7 @@ __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char
     gemm_epilogue<EPI, INT8, MI, NI>(a, acc, row0, col0, h, i32);
 }
 
-template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int FDB>
+template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int FDB, int MF = 32>
 __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned char *lds,
                                              unsigned char *lds_b) {
     const uint32_t KT = a.k / GBK;
@@ -753,8 +921,8 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     if (pid < ndp) { /* whole tile; ids XCD-remapped over the whole-tile range */
         if ((ndp & 7u) == 0) pid = (pid & 7u) * (ndp >> 3) + (pid >> 3);
         gemm_tile_at(a, pid, tm, tn);
-        gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB>(a, lds, lds_b, tm, tn, 0, KT, acc);
-        gemm_finish<EPI, INT8, WM, WN, MI, NI, PF>(a, lds, lds_b, tm, tn, acc);
+        gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF>(a, lds, lds_b, tm, tn, 0, KT, acc);
+        gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc);
         return;
     }
     /* Piece of a split tile. Pieces are numbered k-range-major, so the
@@ -767,9 +935,9 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     const uint32_t piece = q / R, r = q % R;
     const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
     gemm_tile_at(a, ndp + r, tm, tn);
-    gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB>(a, lds, lds_b, tm, tn, kb, ke, acc);
+    gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF>(a, lds, lds_b, tm, tn, kb, ke, acc);
     float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
-    gemm_finish<EPI, INT8, WM, WN, MI, NI, PF>(a, lds, lds_b, tm, tn, acc,
+    gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc,
                                                slots + (size_t)piece * QW_SPLIT_PART);
     /* publish the partial (its coherent stores complete before the
      * workgroup's barrier), then count it. Agent-scope release/acquire
@@ -785,7 +953,7 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     if (ticket != S - 1) return;
     /* last piece in: the others' partials are read with coherent loads */
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    gemm_finish<EPI, INT8, WM, WN, MI, NI, PF>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S,
+    gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S,
                                                piece);
     if (threadIdx.x == 0)
         __hip_atomic_store(a.sk_flag + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -800,13 +968,15 @@ struct GemmLds {
     static constexpr int BYTES = STAGE > SLABS ? STAGE : SLABS;
 };
 
-#define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI, PF, FDB)                                 \
+#define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI, PF, FDB) \
+    QW_GEMM_ENTRY_MF(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, 32)
+#define QW_GEMM_ENTRY_MF(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, MF)                          \
     QW_KERNEL void __launch_bounds__(64 * WM * WN, 1) name(qw_gemm_args a) {                 \
         __shared__ __attribute__((aligned(16))) unsigned char                                \
             lds[PF == 0 ? GemmLds<WM, WN, MI, NI>::BYTES : 2 * GemmShape<WM, WN, MI, NI>::STAGE]; \
         __shared__ __attribute__((aligned(16)))                                               \
             unsigned char lds_b[PF == 0 ? GemmLds<WM, WN, MI, NI>::BYTES : 16];              \
-        qw_gemm_impl<EPI, INT8, WM, WN, MI, NI, PF, FDB>(a, lds, lds_b);                          \
+        qw_gemm_impl<EPI, INT8, WM, WN, MI, NI, PF, FDB, MF>(a, lds, lds_b);                      \
     }
 
 /* shape A: 4 waves, 128 x 128 per wave */
@@ -834,3 +1004,11 @@ QW_GEMM_ENTRY(qw_gemm_i8_gelu_w8, QW_EPI_GELU, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FD
 QW_GEMM_ENTRY(qw_gemm_i8_gate_w8, QW_EPI_GATE, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
 QW_GEMM_ENTRY(qw_gemm_bf16_qkn_w8, QW_EPI_QKNORM, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
 QW_GEMM_ENTRY(qw_gemm_i8_qkn_w8, QW_EPI_QKNORM, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
+/* shape d (default): the geometry of b (8 waves of 64 x 128) with
+ * v_mfma_f32_16x16x32_bf16, bf16 weights (int8 weights widened first); the
+ * in-loop-widening int8 kernels are b's. (The same MFMA with a's geometry,
+ * 4 waves of 128 x 128, measured 20-30% slower than b and is not built.) */
+QW_GEMM_ENTRY_MF(qw_gemm_bf16_store_d, QW_EPI_STORE, 0, 4, 2, 2, 4, 0, 1, 16)
+QW_GEMM_ENTRY_MF(qw_gemm_bf16_gelu_d, QW_EPI_GELU, 0, 4, 2, 2, 4, 0, 1, 16)
+QW_GEMM_ENTRY_MF(qw_gemm_bf16_gate_d, QW_EPI_GATE, 0, 4, 2, 2, 4, 0, 1, 16)
+QW_GEMM_ENTRY_MF(qw_gemm_bf16_qkn_d, QW_EPI_QKNORM, 0, 4, 2, 2, 4, 0, 1, 16)
