@@ -343,8 +343,14 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx1
                     y[2 * j + 1] = hi_bf(rv[j]) + y[2 * j + 1] * hi_bf(gv[j]);
                 }
             }
-            *(u32x4 *)dst = u32x4{pack_bf(y[0], y[1]), pack_bf(y[2], y[3]), pack_bf(y[4], y[5]),
-                                  pack_bf(y[6], y[7])};
+#ifdef QW_EXP_EPI_NOSTORE /* experiments only: everything but the store */
+            if (a.ldc != 0x7FFFFFFFu) continue;
+#endif
+            /* non-temporal store: measured 3% faster on the up projection
+             * and 8% on 8192^3 than a default-policy store */
+            __builtin_nontemporal_store(u32x4{pack_bf(y[0], y[1]), pack_bf(y[2], y[3]),
+                                              pack_bf(y[4], y[5]), pack_bf(y[6], y[7])},
+                                        (u32x4 *)dst);
         }
     }
 }
