@@ -1,9 +1,10 @@
 /* Block-causal prefix flash attention, D = 128, on CDNA4 matrix cores.
  *
- * One workgroup = 4 waves = 128 query rows of one (batch, head); each wave
- * owns 32 queries; two workgroups share a CU. The loop is software
- * pipelined: the QK MFMAs of tile t + 1 are issued before the softmax of
- * tile t, so that VALU work can issue under them.
+ * One workgroup = QW_ATTN_WAVES waves (8: 256 query rows of one (batch,
+ * head), one workgroup per CU, two waves per SIMD); each wave owns 32
+ * queries. The loop is software pipelined: the QK MFMAs of tile t + 1 are
+ * issued between the VALU instructions of tile t's softmax (the first
+ * 32-key block under the tile max, the second under the exp / convert).
  *
  * Scores are computed transposed, S^T = K Q^T, with
  * v_mfma_f32_32x32x16_bf16: in that output layout each lane holds ONE query
@@ -72,8 +73,13 @@ __device__ __forceinline__ float attn_exp(const floatx16 (&s)[AKB], bf16x8 (&pf)
         const int kbk = tk >> 1, v0 = 8 * (tk & 1);
 #pragma unroll
         for (int u = 0; u < 8; u += 2) {
+#ifdef QW_EXP_ATT_NOEXP /* experiments only (like QW_EXP_ATT_NOK / NOV / FIXKV) */
+            const float p0 = __builtin_fmaf(s[kbk][v0 + u], c, -m_use);
+            const float p1 = __builtin_fmaf(s[kbk][v0 + u + 1], c, -m_use);
+#else
             const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kbk][v0 + u], c, -m_use));
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kbk][v0 + u + 1], c, -m_use));
+#endif
             const qw_b2 pp = __builtin_bit_cast(qw_b2, pack_bf(p0, p1));
             pf[tk][u] = pp[0];
             pf[tk][u + 1] = pp[1];
@@ -195,6 +201,10 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
     const uint32_t drow = lane >> 4, dphys = lane & 15;
     auto issue = [&](uint32_t kstage, uint32_t kv0k, uint32_t vstage, uint32_t kv0v)
         __attribute__((always_inline)) {
+#ifdef QW_EXP_ATT_FIXKV
+        kv0k = 0;
+        kv0v = 0;
+#endif
 #pragma unroll
         for (int jj = 0; jj < DPW; jj++) {
             const uint32_t blk = wave * DPW + jj;     /* 1 KB block of the tile */
@@ -207,19 +217,24 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
                      (kvv * a.ldv + ((dphys ^ (4 * (row & 3))) * 8)) * 2);
         }
     };
-    /* S^T of one tile: keys kv0 + 32 kbk + [0, 32) */
-    auto qk = [&](uint32_t kstage, floatx16 (&s)[AKB]) __attribute__((always_inline)) {
+    /* S^T of one tile: keys kv0 + 32 kbk + [0, 32), one MFMA per 16-d step;
+     * steps [i0, i1) of the 8 AKB (kbk, st) pairs, kbk-major */
+    auto qk = [&](uint32_t kstage, floatx16 (&s)[AKB], int i0, int i1) __attribute__((always_inline)) {
         const unsigned char *ks = lds + kstage * A_TILE;
 #pragma unroll
-        for (int kbk = 0; kbk < AKB; kbk++) {
+        for (int i = i0; i < i1; i++) {
+            const int kbk = i / 8, st = i % 8;
+            if (st == 0) {
 #pragma unroll
-            for (int v = 0; v < 16; v++) s[kbk][v] = 0.0f;
-#pragma unroll
-            for (int st = 0; st < 8; st++) {
-                const bf16x8 kf = *(const bf16x8 *)(ks + (kbk * 32 + j) * 256 +
-                                                    (((2 * st + h) ^ (j & 15)) << 4));
-                s[kbk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kbk], 0, 0, 0);
+                for (int v = 0; v < 16; v++) s[kbk][v] = 0.0f;
             }
+#ifdef QW_EXP_ATT_NOK
+            const bf16x8 kf = qf[(st + 1) & 7];
+#else
+            const bf16x8 kf = *(const bf16x8 *)(ks + (kbk * 32 + j) * 256 +
+                                                (((2 * st + h) ^ (j & 15)) << 4));
+#endif
+            s[kbk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kbk], 0, 0, 0);
         }
     };
     /* V^T operand by transposing reads (ds_read_b64_tr_b16): in each 16-lane
@@ -242,7 +257,11 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
                     (attn_lds_b4 *)(vs + r0 * 256 + ((cc ^ (4 * (r0 & 3))) << 4) + half * 8));
                 const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
                     (attn_lds_b4 *)(vs + r1 * 256 + ((cc ^ (4 * (r1 & 3))) << 4) + half * 8));
+#ifdef QW_EXP_ATT_NOV
+                const bf16x8 vf = qf[(tk + db) & 7];
+#else
                 const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+#endif
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[tk], o[db], 0, 0, 0);
             }
         }
@@ -250,22 +269,35 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
 
     float m_run = -INFINITY, l_run = 0.0f;
     const float c = a.scale_log2;
-    /* Online-softmax step of a tile whose S is in `sc`: lazy running max
-     * (it moves only when a row's tile max exceeds it by more than 2^8, or
-     * on the first finite max, so p <= 256 and O, l stay consistent; a move
-     * rescales and redoes the tile's P), bf16 P, row sum. */
-    auto softmax = [&](floatx16 (&sc)[AKB], bf16x8 (&pf)[2 * AKB], uint32_t kv0)
-        __attribute__((always_inline)) {
+    /* Online-softmax step of a tile whose S is in `sc`, with the QK MFMAs of
+     * the next tile (into `sn`) laid out between its VALU work. The running
+     * max moves lazily: only when a row's tile max exceeds it by more than
+     * 2^8, or on the first finite max, so p <= 256; a move rescales O and l
+     * first (a rare, wave-uniform branch). Then P = bf16(exp2(S c - m)) and
+     * the row sum, once. */
+    /* QK MFMAs issued under the tile max, VALU instructions placed after
+     * each later QK MFMA (measured: 8 and 4 beat 2, 4 and 3, 6, 8) */
+    constexpr int QK_PRE = 8, QK_NV = 4;
+    auto softmax_qk = [&](floatx16 (&sc)[AKB], bf16x8 (&pf)[2 * AKB], uint32_t kv0,
+                          uint32_t kstage_next, floatx16 (&sn)[AKB]) __attribute__((always_inline)) {
         if (kv0 + AKT > lmin) attn_mask(sc, kv0, L, h);
+        /* the first QK MFMAs of the next tile run under the tile max */
+        qk(kstage_next, sn, 0, QK_PRE);
         float mt = -INFINITY;
 #pragma unroll
         for (int kbk = 0; kbk < AKB; kbk++)
 #pragma unroll
             for (int v = 0; v < 16; v++) mt = fmaxf(mt, sc[kbk][v]);
         mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int i = 0; i < QK_PRE; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            if (i + 2 < QK_PRE) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
         const float m_new = mt * c;
         const bool move = m_new > m_run + 8.0f;
-        float rs = attn_exp(sc, pf, c, m_run == -INFINITY ? 0.0f : m_run);
         if (__builtin_amdgcn_ballot_w64(move)) {
             const float m_to = move ? m_new : m_run;
             const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_to);
@@ -275,7 +307,17 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
 #pragma unroll
                 for (int v = 0; v < 16; v++) o[db][v] *= alpha;
             m_run = m_to;
-            rs = attn_exp(sc, pf, c, m_run == -INFINITY ? 0.0f : m_run);
+        }
+        float rs = attn_exp(sc, pf, c, m_run == -INFINITY ? 0.0f : m_run);
+        qk(kstage_next, sn, QK_PRE, 8 * AKB);
+        /* K fragment reads run two MFMAs ahead; the exp, convert and sum
+         * VALU fills the issue slots between MFMAs */
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+        for (int i = QK_PRE; i < 8 * AKB; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, QK_NV, 0);
+            if (i + 2 < 8 * AKB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
         rs += __shfl_xor(rs, 32, 64);
         l_run += rs;
@@ -289,7 +331,7 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
     }
     __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0) */
     attn_barrier();
-    if (ntiles) qk(0, s0);
+    if (ntiles) qk(0, s0, 0, 8 * AKB);
     /* One tile: issue K(t + 2) and V(t + 1) into the stages tile t - 1 used
      * (their readers passed the previous barrier), QK of tile t + 1, the
      * softmax and P.V of tile t, then wait for the issued tiles and
@@ -298,9 +340,8 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
         __attribute__((always_inline)) {
         const uint32_t kv0 = t * AKT;
         issue(t & 1, kv0 + 2 * AKT, (t + 1) & 1, kv0 + AKT);
-        qk((t + 1) & 1, sn);
         bf16x8 pf[2 * AKB];
-        softmax(sc, pf, kv0);
+        softmax_qk(sc, pf, kv0, (t + 1) & 1, sn);
         pv(t & 1, pf);
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): K(t + 2), V(t + 1) landed */
         attn_barrier();
