@@ -1019,6 +1019,19 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
             grid = a.dp_tiles + R * s;
         }
     }
+    {
+        static int persist = -1;
+        if (persist < 0) {
+            const char *e = getenv("QW_GEMM_PERSIST");
+            persist = !(e && e[0] == '0');
+        }
+        /* shape d without split tiles: one workgroup per CU walks the tiles,
+         * so a tile's output stores drain under the next tile's first loads
+         * (up 521 -> 514 us, QKV 365 -> 359 us; QW_GEMM_PERSIST=0: one
+         * workgroup per tile) */
+        if (persist && shape == 'd' && a.split == 1 && grid > g->cus && g->cus % 8 == 0)
+            grid = g->cus;
+    }
     if (!launch(g, kid, dim3(grid), dim3(threads), a)) return 0;
     if (qkn_after)
         return qw_gpu_qk_norm_rope_bf16(g, d->out, d->rows, d->cols / 384, d->ldc, d->cols / 3,

@@ -948,6 +948,23 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     floatx16 acc[NI][MI]; /* C^T blocks */
     uint32_t pid = blockIdx.x, tm, tn;
     if (pid < ndp) { /* whole tile; ids XCD-remapped over the whole-tile range */
+        if (MF == 16 && !split) {
+            /* a grid smaller than the tile count walks the tiles in strides
+             * of the grid (the host launches one workgroup per CU); each
+             * tile's epilogue stores drain under the next tile's first
+             * loads. The XCD of id and of id + grid agree (grid % 8 == 0). */
+            for (uint32_t id = pid; id < ndp; id += gridDim.x) {
+                uint32_t q = id;
+                if ((ndp & 7u) == 0) q = (q & 7u) * (ndp >> 3) + (q >> 3);
+                gemm_tile_at(a, q, tm, tn);
+                gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF>(a, lds, lds_b, tm, tn, 0, KT, acc);
+                gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc);
+                /* every wave's slab reads done before the next tile's loads
+                 * land in the stages (stores may stay in flight) */
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            }
+            return;
+        }
         if ((ndp & 7u) == 0) pid = (pid & 7u) * (ndp >> 3) + (pid >> 3);
         gemm_tile_at(a, pid, tm, tn);
         gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF>(a, lds, lds_b, tm, tn, 0, KT, acc);
