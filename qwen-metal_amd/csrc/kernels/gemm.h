@@ -93,6 +93,13 @@ __device__ __forceinline__ void gemm_tile_at(const qw_gemm_args &a, uint32_t pid
 #ifndef QW_GEMM_GROUP
 #define QW_GEMM_GROUP 8
 #endif
+#ifdef QW_EXP_ROWMAJOR
+    if (a.tiles_n <= QW_EXP_ROWMAJOR) {
+        tm = pid / a.tiles_n;
+        tn = pid % a.tiles_n;
+        return;
+    }
+#endif
     const uint32_t G = QW_GEMM_GROUP;
     const uint32_t per_group = G * a.tiles_n;
     const uint32_t first_m = (pid / per_group) * G;
@@ -509,9 +516,10 @@ __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &
 }
 
 /* Instructions of one kind placed after MFMA i of n: one each after the
- * first `count` MFMAs, or spread evenly when there are more than MFMAs */
-__device__ constexpr int sched_share(int count, int n, int i) {
-    return count <= n ? (i < count ? 1 : 0) : count * (i + 1) / n - count * i / n;
+ * first `count` MFMAs, or spread evenly (always when there are more than
+ * MFMAs, or when `spread`) */
+__device__ constexpr int sched_share(int count, int n, int i, bool spread = false) {
+    return count <= n && !spread ? (i < count ? 1 : 0) : count * (i + 1) / n - count * i / n;
 }
 
 /* 16 x 16 block q (0..3) of a 32 x 32 accumulator's registers (elements
@@ -530,7 +538,7 @@ __device__ __forceinline__ void mfma16_into(floatx16 &acc, int q, bf16x8 a, bf16
  * (nb, mb) of C^T in quarter 2 (nb % 2) + mb % 2 of acc[nb / 2][mb / 2];
  * the second sub-step is held back to the start of the next slice (PREV). */
 template <int INT8, int MI, int NI, int A_BYTES, int A_DL, int W_DL, int WLD, int WROWS,
-          bool PREV>
+          bool PREV, bool SPREAD = false>
 __device__ __forceinline__ void gemm_pipe_slice16(const PipeCtx<A_DL, W_DL, WLD> &c,
                                                   floatx16 (&acc)[NI][MI], bf16x8 (&pa)[2 * MI],
                                                   bf16x8 (&pw)[2 * NI],
@@ -608,7 +616,7 @@ __device__ __forceinline__ void gemm_pipe_slice16(const PipeCtx<A_DL, W_DL, WLD>
             for (int q = 0; q < sched_share(NV, NMF, i); q++)
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
 #pragma unroll
-            for (int q = 0; q < sched_share(NRD, NMF, i); q++)
+            for (int q = 0; q < sched_share(NRD, NMF, i, SPREAD); q++)
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     } else {
@@ -619,7 +627,7 @@ __device__ __forceinline__ void gemm_pipe_slice16(const PipeCtx<A_DL, W_DL, WLD>
     for (int i = 0; i < NMF; i++) { /* step 0: fragments of step 1, int8 W writes */
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
 #pragma unroll
-        for (int q = 0; q < sched_share(NRD, NMF, i); q++)
+        for (int q = 0; q < sched_share(NRD, NMF, i, SPREAD); q++)
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
 #pragma unroll
         for (int q = 0; q < sched_share(NW, NMF, i); q++)
@@ -630,7 +638,7 @@ __device__ __forceinline__ void gemm_pipe_slice16(const PipeCtx<A_DL, W_DL, WLD>
 /* Sums of tile (tm, tn) over k-steps [kb, ke) (64 k each) into acc; the
  * PF == 1, 2 pipelines take the whole k range only. Ends with the LDS
  * stages free (after a barrier). */
-template <int INT8, int WM, int WN, int MI, int NI, int PF, int FDB, int MF = 32>
+template <int INT8, int WM, int WN, int MI, int NI, int PF, int FDB, int MF = 32, bool SPREAD = false>
 __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned char *lds,
                                               unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                               uint32_t kb, uint32_t ke,
@@ -809,7 +817,7 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
             bf16x8 pa[2 * MI], pw[2 * NI]; /* last sub-step's fragments, multiplied one slice late */
             {
                 const uint32_t nk = (kb + 1 < KT ? kb + 1 : kb) * GBK;
-                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, false>(
+                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, false, SPREAD>(
                     c, acc, pa, pw, lds, lds_b, QW_K(nk));
                 QW_SLICE_END();
             }
@@ -817,15 +825,15 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
              * time and their LDS bases fold into the instructions' offsets */
             uint32_t kt = kb + 1;
             for (; kt + 1 < KT; kt += 2) {
-                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true, SPREAD>(
                     c, acc, pa, pw, lds_b, lds, QW_K((kt + 1) * GBK));
                 QW_SLICE_END();
-                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true, SPREAD>(
                     c, acc, pa, pw, lds, lds_b, QW_K((kt + 2 < KT ? kt + 2 : kt + 1) * GBK));
                 QW_SLICE_END();
             }
             if (kt < KT) { /* the last slice, from stage lds_b */
-                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
+                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true, SPREAD>(
                     c, acc, pa, pw, lds_b, lds, QW_K(kt * GBK));
                 QW_SLICE_END();
             }
@@ -938,7 +946,8 @@ __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char
     gemm_epilogue<EPI, INT8, MI, NI>(a, acc, row0, col0, h, i32);
 }
 
-template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int FDB, int MF = 32>
+template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int FDB, int MF = 32,
+          bool SPREAD = false>
 __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned char *lds,
                                              unsigned char *lds_b) {
     const uint32_t KT = a.k / GBK;
@@ -957,7 +966,7 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
                 uint32_t q = id;
                 if ((ndp & 7u) == 0) q = (q & 7u) * (ndp >> 3) + (q >> 3);
                 gemm_tile_at(a, q, tm, tn);
-                gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF>(a, lds, lds_b, tm, tn, 0, KT, acc);
+                gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD>(a, lds, lds_b, tm, tn, 0, KT, acc);
                 gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc);
                 /* every wave's slab reads done before the next tile's loads
                  * land in the stages (stores may stay in flight) */
@@ -967,7 +976,7 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
         }
         if ((ndp & 7u) == 0) pid = (pid & 7u) * (ndp >> 3) + (pid >> 3);
         gemm_tile_at(a, pid, tm, tn);
-        gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF>(a, lds, lds_b, tm, tn, 0, KT, acc);
+        gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD>(a, lds, lds_b, tm, tn, 0, KT, acc);
         gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc);
         return;
     }
@@ -981,7 +990,7 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     const uint32_t piece = q / R, r = q % R;
     const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
     gemm_tile_at(a, ndp + r, tm, tn);
-    gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF>(a, lds, lds_b, tm, tn, kb, ke, acc);
+    gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD>(a, lds, lds_b, tm, tn, kb, ke, acc);
     float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
     gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc,
                                                slots + (size_t)piece * QW_SPLIT_PART);
@@ -1016,13 +1025,15 @@ struct GemmLds {
 
 #define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI, PF, FDB) \
     QW_GEMM_ENTRY_MF(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, 32)
-#define QW_GEMM_ENTRY_MF(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, MF)                          \
+#define QW_GEMM_ENTRY_MF(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, MF) \
+    QW_GEMM_ENTRY_SP(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, MF, false)
+#define QW_GEMM_ENTRY_SP(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD)                  \
     QW_KERNEL void __launch_bounds__(64 * WM * WN, 1) name(qw_gemm_args a) {                 \
         __shared__ __attribute__((aligned(16))) unsigned char                                \
             lds[PF == 0 ? GemmLds<WM, WN, MI, NI>::BYTES : 2 * GemmShape<WM, WN, MI, NI>::STAGE]; \
         __shared__ __attribute__((aligned(16)))                                               \
             unsigned char lds_b[PF == 0 ? GemmLds<WM, WN, MI, NI>::BYTES : 16];              \
-        qw_gemm_impl<EPI, INT8, WM, WN, MI, NI, PF, FDB, MF>(a, lds, lds_b);                      \
+        qw_gemm_impl<EPI, INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD>(a, lds, lds_b);              \
     }
 
 /* shape A: 4 waves, 128 x 128 per wave */
@@ -1055,6 +1066,6 @@ QW_GEMM_ENTRY(qw_gemm_i8_qkn_w8, QW_EPI_QKNORM, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_F
  * in-loop-widening int8 kernels are b's. (The same MFMA with a's geometry,
  * 4 waves of 128 x 128, measured 20-30% slower than b and is not built.) */
 QW_GEMM_ENTRY_MF(qw_gemm_bf16_store_d, QW_EPI_STORE, 0, 4, 2, 2, 4, 0, 1, 16)
-QW_GEMM_ENTRY_MF(qw_gemm_bf16_gelu_d, QW_EPI_GELU, 0, 4, 2, 2, 4, 0, 1, 16)
-QW_GEMM_ENTRY_MF(qw_gemm_bf16_gate_d, QW_EPI_GATE, 0, 4, 2, 2, 4, 0, 1, 16)
+QW_GEMM_ENTRY_SP(qw_gemm_bf16_gelu_d, QW_EPI_GELU, 0, 4, 2, 2, 4, 0, 1, 16, true)
+QW_GEMM_ENTRY_SP(qw_gemm_bf16_gate_d, QW_EPI_GATE, 0, 4, 2, 2, 4, 0, 1, 16, true)
 QW_GEMM_ENTRY_MF(qw_gemm_bf16_qkn_d, QW_EPI_QKNORM, 0, 4, 2, 2, 4, 0, 1, 16)
