@@ -962,17 +962,22 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     const int qkn = d->epilogue == QW_LINEAR_QKNORM;
     /* the fused q/k epilogue exists for shapes b and d; a and r store and
      * run the separate norm + rope kernel afterwards */
-    const int qkn_after = qkn && (shape == 'a' || shape == 'r');
+    static int qkn_fused = -1;
+    if (qkn_fused < 0) {
+        const char *e = getenv("QW_QKN_FUSED");
+        qkn_fused = !(e && e[0] == '0');
+    }
+    const int qkn_after = qkn && (shape == 'a' || shape == 'r' || !qkn_fused);
     int kid = (int8 && !widen ? K_GEMM_I8_STORE : K_GEMM_BF16_STORE) +
               (qkn ? QW_LINEAR_STORE : d->epilogue);
     unsigned threads = 256, bm = 256, bn = 256;
     if (shape == 'b') {
         kid += K_GEMM_BF16_STORE_W8 - K_GEMM_BF16_STORE;
         threads = 512;
-        if (qkn) kid = int8 && !widen ? K_GEMM_I8_QKN_W8 : K_GEMM_BF16_QKN_W8;
+        if (qkn && !qkn_after) kid = int8 && !widen ? K_GEMM_I8_QKN_W8 : K_GEMM_BF16_QKN_W8;
     } else if (shape == 'd') { /* b's geometry with 16x16x32 MFMAs */
         kid += K_GEMM_BF16_STORE_D - K_GEMM_BF16_STORE;
-        if (qkn) kid = K_GEMM_BF16_QKN_D;
+        if (qkn && !qkn_after) kid = K_GEMM_BF16_QKN_D;
         threads = 512;
     } else if (shape == 'r') {
         kid += K_GEMM_BF16_STORE_R - K_GEMM_BF16_STORE;
