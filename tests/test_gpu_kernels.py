@@ -226,6 +226,40 @@ def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
     assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
+@pytest.mark.parametrize("epi", ["store", "gelu"])
+def test_linear_tile_walk(gpu, qd, oracle, epi):
+    """More tiles than compute units: the 16x16x32 GEMM launches one
+    workgroup per CU and each walks its tiles in strides of the grid. 17 x
+    17 tiles of 256 x 256 (289 > 256), ragged in both the last tile row
+    (4100 rows) and the last tile column (4104 columns), called twice in a
+    row (the workgroups keep no state between tiles or calls)."""
+    rows, k, n = 4100, 256, 4104
+    x = synth(oracle, rows * k, 41)
+    w = synth(oracle, n * k, 42, 0.02)
+    b = synth(oracle, n, 43, 0.02)
+    xt, wt, bt = gpu.put(x), gpu.put(w), gpu.put(b)
+    outs = []
+    for _ in range(2):
+        out = gpu.new(rows * n, qd.BF16)
+        gpu.linear(out, xt, wt, rows, k, n, bias=bt,
+                   epilogue=qd.LINEAR_GELU if epi == "gelu" else qd.LINEAR_STORE)
+        gpu.submit()
+        outs.append(out.read())
+    assert np.array_equal(outs[0], outs[1])
+    lin = oracle.linear(x, w, b, rows, k, n).ravel()
+    absx, absw = x & np.uint16(0x7FFF), w & np.uint16(0x7FFF)
+    mag = oracle.bf16_to_f32(oracle.linear(absx, absw, None, rows, k, n)).ravel()
+    if epi == "store":
+        assert_linear_close(oracle, outs[0], lin, mag)
+        return
+    want = np.empty_like(lin)
+    oracle.lib().qo_gelu_tanh(want, lin, lin.size)
+    d = ulp_diff(outs[0], want)
+    diff = np.abs(oracle.bf16_to_f32(outs[0]).astype(np.float64) - oracle.bf16_to_f32(want))
+    ok = (d <= 2) | (diff <= 2.0 ** -13 * mag)
+    assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
+
+
 @pytest.mark.parametrize("rows,int8,rope_rows", [(300, False, 300), (300, True, 150),
                                                  (1000, True, 500), (4357, False, 4357)])
 def test_linear_qknorm_epilogue_bit_identical(gpu, qd, oracle, rows, int8, rope_rows):
