@@ -31,7 +31,8 @@ enum {
     K_GEMM_I8_QKN_W8,
     K_GEMM_BF16_STORE_D, K_GEMM_BF16_GELU_D, K_GEMM_BF16_GATE_D, K_GEMM_BF16_QKN_D,
     K_GEMM_BF16_STORE_R, K_GEMM_BF16_GELU_R, K_GEMM_BF16_GATE_R,
-    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA, K_COUNT
+    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
+    K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_bf16", "qw_rms_norm_one_bf16", "qw_qk_norm_rope_bf16",
@@ -46,7 +47,8 @@ static const char *k_names[K_COUNT] = {
     "qw_gemm_bf16_store_d", "qw_gemm_bf16_gelu_d", "qw_gemm_bf16_gate_d", "qw_gemm_bf16_qkn_d",
     "qw_gemm_bf16_store_r", "qw_gemm_bf16_gelu_r", "qw_gemm_bf16_gate_r",
     "qw_gemm_i8_store_r", "qw_gemm_i8_gelu_r", "qw_gemm_i8_gate_r", "qw_widen_i8_bf16",
-    "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16"};
+    "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16",
+    "qw_gemv_bf16_store", "qw_gemv_bf16_gelu", "qw_gemv_i8_store", "qw_gemv_i8_gelu"};
 
 struct h3_gpu {
     int device;
@@ -823,12 +825,18 @@ static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps) {
         if (mode < 0) mode = 0;
     }
     if (mode <= 1) return 1;
+    static int min_env = -1;
+    if (min_env < 0) {
+        const char *e = getenv("QW_GEMM_SPLIT_MIN");
+        min_env = e && e[0] ? atoi(e) : 0;
+    }
+    const uint32_t min_steps = min_env > 0 ? (uint32_t)min_env : 32;
     const uint32_t G = g->cus, R = tiles % G;
     if (R == 0) return 1;
     uint32_t best = 1;
     double best_t = 0.9;
     for (uint32_t s = 2; s <= 8; s++) {
-        if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * G || ksteps < 32 * s) break;
+        if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * G || ksteps < min_steps * s) break;
         if (mode != 9999) {
             if (s == (uint32_t)mode) return s;
             continue;
@@ -901,6 +909,32 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
             return fail(g, "linear qk: tensors must be 16-byte aligned");
     } else if (d->epilogue != QW_LINEAR_STORE && d->epilogue != QW_LINEAR_GELU) {
         return fail(g, "linear: unknown epilogue %d", d->epilogue);
+    }
+    /* at most 8 rows, plain or GELU epilogue: one wave per 2 output columns
+     * streams the weight once (QW_GEMV=0 sends these to the tiled kernels) */
+    static int gemv = -1;
+    if (gemv < 0) {
+        const char *e = getenv("QW_GEMV");
+        gemv = !(e && e[0] == '0');
+    }
+    if (gemv && d->rows <= 8 &&
+        (d->epilogue == QW_LINEAR_STORE || d->epilogue == QW_LINEAR_GELU)) {
+        qw_gemm_args a;
+        memset(&a, 0, sizeof(a));
+        a.a = (const uint16_t *)d->in->ptr + d->in_offset;
+        a.w = d->weight->ptr;
+        a.wscale = d->wscale ? (const float *)d->wscale->ptr : NULL;
+        a.bias = d->bias ? (const uint16_t *)d->bias->ptr : NULL;
+        a.out = (uint16_t *)d->out->ptr + d->out_offset;
+        a.m = d->rows;
+        a.n = d->cols;
+        a.k = d->k;
+        a.lda = d->lda;
+        a.ldc = d->ldc;
+        const int kid = (int8 ? K_GEMV_I8_STORE : K_GEMV_BF16_STORE) +
+                        (d->epilogue == QW_LINEAR_GELU ? 1 : 0);
+        const uint32_t waves = (d->cols + 1) / 2; /* 2 columns per wave */
+        return launch(g, kid, dim3((waves + 3) / 4), dim3(256), a);
     }
     /* int8 weights with many rows: widen the weight to bf16 once (exact,
      * unscaled) and run the bf16 GEMM, whose epilogue applies the per-row

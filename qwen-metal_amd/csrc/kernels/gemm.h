@@ -84,6 +84,91 @@ QW_KERNEL void __launch_bounds__(256) qw_widen_i8_bf16(qw_widen_args a) {
     }
 }
 
+/* Linears with at most QW_GEMV_MAX_ROWS rows (the timestep / modulation
+ * MLP runs on 1-2 rows): a 256 x 256 tile would be almost all padding and
+ * its K loop latency-bound, so each wave instead streams QW_GEMV_COLS weight
+ * rows (bf16, or int8 widened in registers) once, 16 bytes per lane, against
+ * the same k chunks of every input row, with fp32 FMAs and a wave-shuffle
+ * sum. The epilogue is the GEMM's: y = bf16(acc * wscale + bias) (the int8
+ * scale multiplies the finished sum, as in the tiled kernels), then GELU or
+ * a plain store. */
+#define QW_GEMV_MAX_ROWS 8
+#define QW_GEMV_COLS 2
+template <int INT8, int EPI>
+__device__ __forceinline__ void qw_gemv_impl(const qw_gemm_args &a) {
+#pragma clang fp contract(off)
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t c0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * QW_GEMV_COLS;
+    if (c0 >= a.n) return; /* whole waves */
+    const uint32_t m = a.m, kc = a.k / 8;
+    const u16 *A = (const u16 *)a.a;
+    float acc[QW_GEMV_MAX_ROWS][QW_GEMV_COLS];
+#pragma unroll
+    for (int r = 0; r < QW_GEMV_MAX_ROWS; r++)
+#pragma unroll
+        for (int c = 0; c < QW_GEMV_COLS; c++) acc[r][c] = 0.0f;
+    for (uint32_t j = lane; j < kc; j += 64) {
+        float w[QW_GEMV_COLS][8];
+#pragma unroll
+        for (int c = 0; c < QW_GEMV_COLS; c++) {
+            const uint32_t col = min(c0 + c, a.n - 1);
+            if (INT8) {
+                const u32x2 q = *(const u32x2 *)((const int8_t *)a.w + (size_t)col * a.k + 8 * j);
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int32_t x = (int32_t)q[h];
+                    w[c][4 * h] = (float)((x << 24) >> 24);
+                    w[c][4 * h + 1] = (float)((x << 16) >> 24);
+                    w[c][4 * h + 2] = (float)((x << 8) >> 24);
+                    w[c][4 * h + 3] = (float)(x >> 24);
+                }
+            } else {
+                const u32x4 q = *(const u32x4 *)((const u16 *)a.w + (size_t)col * a.k + 8 * j);
+#pragma unroll
+                for (int i = 0; i < 4; i++) w[c][2 * i] = lo_bf(q[i]), w[c][2 * i + 1] = hi_bf(q[i]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < QW_GEMV_MAX_ROWS; r++) {
+            if ((uint32_t)r >= m) break;
+            const u32x4 x = *(const u32x4 *)(A + (size_t)r * a.lda + 8 * j);
+            float xf[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) xf[2 * i] = lo_bf(x[i]), xf[2 * i + 1] = hi_bf(x[i]);
+#pragma unroll
+            for (int c = 0; c < QW_GEMV_COLS; c++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[r][c] = fmaf(xf[i], w[c][i], acc[r][c]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < QW_GEMV_MAX_ROWS; r++) {
+        if ((uint32_t)r >= m) break;
+#pragma unroll
+        for (int c = 0; c < QW_GEMV_COLS; c++) {
+            float t = wave_sum(acc[r][c]);
+            const uint32_t col = c0 + c;
+            if (lane != 0 || col >= a.n) continue;
+            if (a.wscale) t *= a.wscale[col];
+            float y = bf2f(f2bf(t + (a.bias ? bf2f(a.bias[col]) : 0.0f)));
+            if (EPI == QW_EPI_GELU) y = gelu_tanh_f(y);
+            a.out[(size_t)r * a.ldc + col] = f2bf(y);
+        }
+    }
+}
+QW_KERNEL void __launch_bounds__(256) qw_gemv_bf16_store(qw_gemm_args a) {
+    qw_gemv_impl<0, QW_EPI_STORE>(a);
+}
+QW_KERNEL void __launch_bounds__(256) qw_gemv_bf16_gelu(qw_gemm_args a) {
+    qw_gemv_impl<0, QW_EPI_GELU>(a);
+}
+QW_KERNEL void __launch_bounds__(256) qw_gemv_i8_store(qw_gemm_args a) {
+    qw_gemv_impl<1, QW_EPI_STORE>(a);
+}
+QW_KERNEL void __launch_bounds__(256) qw_gemv_i8_gelu(qw_gemm_args a) {
+    qw_gemv_impl<1, QW_EPI_GELU>(a);
+}
+
 /* Workgroup id -> (tile row, tile column). Ids are dealt round-robin to the
  * 8 XCDs; the id is remapped so each XCD owns a contiguous range of tiles,
  * walked in groups of 8 tile-rows (column-major inside a group), so the A

@@ -86,6 +86,10 @@ LINEAR_CASES = [
     (37, 256, 136, True, True),     # int8 widened inside the GEMM loop
     (700, 512, 264, False, True),
     (2, 3072, 12288, True, False),
+    # at most 8 rows: the streaming GEMV kernels (bf16 and int8 weights)
+    (3, 3072, 3072, True, False),
+    (8, 512, 1032, True, True),
+    (1, 3072, 18432, False, True),
 ]
 
 
@@ -113,7 +117,8 @@ def test_linear_store(gpu, qd, oracle, rows, k, n, bias, int8):
     assert_linear_close(oracle, got, ref.ravel(), mag)
 
 
-@pytest.mark.parametrize("int8,rows", [(False, 300), (True, 300), (True, 600)])
+@pytest.mark.parametrize("int8,rows", [(False, 300), (True, 300), (True, 600), (False, 4),
+                                       (True, 7)])
 def test_linear_gelu_and_gate_epilogues(gpu, qd, oracle, int8, rows):
     k, n = 512, 768
     x = synth(oracle, rows * k, 4)
