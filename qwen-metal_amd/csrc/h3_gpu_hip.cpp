@@ -814,7 +814,10 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
  * pieces lost more to their partials than they gained (K = 3072 linears
  * measured slower when split, K = 12288 ones faster), and
  * R s <= QW_SPLIT_MAX_PIECES * cus bounds the partial workspace.
- * QW_GEMM_SPLIT=0 (or 1) disables it, =N forces s = N where allowed. */
+ * QW_GEMM_SPLIT=0 (or 1) disables it, =N forces s = N where allowed;
+ * QW_GEMM_SPLIT_MIN=N lowers the minimum piece length to N k-steps (an
+ * experiment switch: at 8-16 it sped up the few-tile linears of the 512^2
+ * loop but slowed the 8704-row out projection). */
 #define QW_SPLIT_MAX_PIECES 2
 static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps) {
     static int mode = -1;
