@@ -24,6 +24,7 @@
 #include <stdint.h>
 
 #include "h3_gpu.h"
+#include "qwen_host.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -97,10 +98,12 @@ enum {
 };
 #define QW_LAYER_STREAM(layer, field) (256ull * (uint64_t)((layer) + 1) + (field))
 
-/* reference qwen_dit.h:77-78: the live weight tensor of one block field,
- * 0 = qkv (fused [3H, H]: q rows, k rows, v rows), 3 = to_out, 4 = fc1,
- * 5 = fc2 (fields 1, 2 also return the fused qkv tensor). int8 weights
- * return the int8 tensor; qw_dit_block_scales gives its fp32 row scales. */
+/* reference qwen_dit.h:84-86: the live weight tensor of one block field,
+ * 0 = to_q, 1 = to_k, 2 = to_v, 3 = to_out, 4 = fc1, 5 = fc2. q, k and v
+ * are non-owning [H, H] row views of the fused [3H, H] weight, owned by the
+ * model (valid until the next LoRA change or qw_dit_free). int8 weights
+ * return the int8 tensor; qw_dit_block_scales gives its fp32 row scales
+ * (for fields 0-2 the [H] slice of the fused scales). */
 const h3_gpu_tensor *qw_dit_block_tensor(const qw_dit *dit, int block,
                                          int field);
 const h3_gpu_tensor *qw_dit_block_scales(const qw_dit *dit, int block,

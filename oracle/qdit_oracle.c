@@ -119,7 +119,7 @@ int qo_schedule_exp_mu(int steps, double exp_mu, double terminal,
                        float *sigma) {
     /* qwen_pipeline.m:130-205 (dynamic shifting branch): every
      * intermediate is a float32 value; exp_mu enters as a double. */
-    if (steps < 1 || steps > 1000 || !sigma) return 0;
+    if (steps < 1 || !sigma) return 0; /* no upper bound, as the reference */
     for (int i = 0; i < steps; i++) {
         double raw = steps == 1 ? 1.0
                                 : 1.0 + (double)i * ((1.0 / steps) - 1.0) /

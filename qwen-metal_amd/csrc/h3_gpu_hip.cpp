@@ -24,14 +24,9 @@
 enum {
     K_LN_MOD, K_RMS_ONE, K_QK_NORM_ROPE, K_GATE, K_ACT, K_SWIGLU, K_CAST,
     K_REORDER, K_FILL, K_QUANT, K_DEQUANT, K_COPY2D, K_ATTN,
-    K_GEMM_BF16_STORE, K_GEMM_BF16_GELU, K_GEMM_BF16_GATE,
-    K_GEMM_I8_STORE, K_GEMM_I8_GELU, K_GEMM_I8_GATE,
-    K_GEMM_BF16_STORE_W8, K_GEMM_BF16_GELU_W8, K_GEMM_BF16_GATE_W8,
-    K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_GEMM_BF16_QKN_W8,
-    K_GEMM_I8_QKN_W8,
-    K_GEMM_BF16_STORE_D, K_GEMM_BF16_GELU_D, K_GEMM_BF16_GATE_D, K_GEMM_BF16_QKN_D,
-    K_GEMM_BF16_STORE_R, K_GEMM_BF16_GELU_R, K_GEMM_BF16_GATE_R,
-    K_GEMM_I8_STORE_R, K_GEMM_I8_GELU_R, K_GEMM_I8_GATE_R, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
+    /* GEMM kernels in QW_LINEAR_* epilogue order (store, gelu, gate, qknorm) */
+    K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_GEMM_I8_QKN_W8,
+    K_GEMM_BF16_STORE_D, K_GEMM_BF16_GELU_D, K_GEMM_BF16_GATE_D, K_GEMM_BF16_QKN_D, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
     K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
@@ -39,14 +34,9 @@ static const char *k_names[K_COUNT] = {
     "qw_gate_bf16", "qw_act_bf16", "qw_swiglu_bf16", "qw_cast_f32_bf16",
     "qw_modulation_reorder_bf16", "qw_fill_normal_bf16", "qw_quantize_int8_rows",
     "qw_dequant_int8_f32", "qw_copy2d", "qw_attention_bf16",
-    "qw_gemm_bf16_store", "qw_gemm_bf16_gelu", "qw_gemm_bf16_gate",
-    "qw_gemm_i8_store", "qw_gemm_i8_gelu", "qw_gemm_i8_gate",
-    "qw_gemm_bf16_store_w8", "qw_gemm_bf16_gelu_w8", "qw_gemm_bf16_gate_w8",
-    "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8",
-    "qw_gemm_bf16_qkn_w8", "qw_gemm_i8_qkn_w8",
+    "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8", "qw_gemm_i8_qkn_w8",
     "qw_gemm_bf16_store_d", "qw_gemm_bf16_gelu_d", "qw_gemm_bf16_gate_d", "qw_gemm_bf16_qkn_d",
-    "qw_gemm_bf16_store_r", "qw_gemm_bf16_gelu_r", "qw_gemm_bf16_gate_r",
-    "qw_gemm_i8_store_r", "qw_gemm_i8_gelu_r", "qw_gemm_i8_gate_r", "qw_widen_i8_bf16",
+    "qw_widen_i8_bf16",
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16",
     "qw_gemv_bf16_store", "qw_gemv_bf16_gelu", "qw_gemv_i8_store", "qw_gemv_i8_gelu"};
 
@@ -813,44 +803,23 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
  * whole-tile tail. Pieces stay at least 32 k-steps (2048 k) long: shorter
  * pieces lost more to their partials than they gained (K = 3072 linears
  * measured slower when split, K = 12288 ones faster), and
- * R s <= QW_SPLIT_MAX_PIECES * cus bounds the partial workspace.
- * QW_GEMM_SPLIT=0 (or 1) disables it, =N forces s = N where allowed;
- * QW_GEMM_SPLIT_MIN=N lowers the minimum piece length to N k-steps (an
- * experiment switch: at 8-16 it sped up the few-tile linears of the 512^2
- * loop but slowed the 8704-row out projection). */
+ * R s <= QW_SPLIT_MAX_PIECES * cus bounds the partial workspace. */
 #define QW_SPLIT_MAX_PIECES 2
 static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps) {
-    static int mode = -1;
-    if (mode < 0) {
-        /* unset, empty or "auto": automatic; 0 or 1: off; N: N pieces */
-        const char *e = getenv("QW_GEMM_SPLIT");
-        mode = !e || !e[0] || !strcmp(e, "auto") ? 9999 : atoi(e);
-        if (mode < 0) mode = 0;
-    }
-    if (mode <= 1) return 1;
-    static int min_env = -1;
-    if (min_env < 0) {
-        const char *e = getenv("QW_GEMM_SPLIT_MIN");
-        min_env = e && e[0] ? atoi(e) : 0;
-    }
-    const uint32_t min_steps = min_env > 0 ? (uint32_t)min_env : 32;
+    const uint32_t min_steps = 32;
     const uint32_t G = g->cus, R = tiles % G;
     if (R == 0) return 1;
     uint32_t best = 1;
     double best_t = 0.9;
     for (uint32_t s = 2; s <= 8; s++) {
         if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * G || ksteps < min_steps * s) break;
-        if (mode != 9999) {
-            if (s == (uint32_t)mode) return s;
-            continue;
-        }
         const double t = (double)((R * s + G - 1) / G) / s + 0.02 * (s - 1);
         if (t < best_t) {
             best_t = t;
             best = s;
         }
     }
-    return mode != 9999 ? 1 : best;
+    return best;
 }
 
 extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
@@ -914,13 +883,8 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
         return fail(g, "linear: unknown epilogue %d", d->epilogue);
     }
     /* at most 8 rows, plain or GELU epilogue: one wave per 2 output columns
-     * streams the weight once (QW_GEMV=0 sends these to the tiled kernels) */
-    static int gemv = -1;
-    if (gemv < 0) {
-        const char *e = getenv("QW_GEMV");
-        gemv = !(e && e[0] == '0');
-    }
-    if (gemv && d->rows <= 8 &&
+     * streams the weight once */
+    if (d->rows <= 8 &&
         (d->epilogue == QW_LINEAR_STORE || d->epilogue == QW_LINEAR_GELU)) {
         qw_gemm_args a;
         memset(&a, 0, sizeof(a));
@@ -942,13 +906,8 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     /* int8 weights with many rows: widen the weight to bf16 once (exact,
      * unscaled) and run the bf16 GEMM, whose epilogue applies the per-row
      * scale to the fp32 sums -- the same arithmetic as the int8 kernels,
-     * without their in-loop widening. QW_I8_FUSED=1 keeps the int8 kernels. */
-    static int fused = -1;
-    if (fused < 0) {
-        const char *e = getenv("QW_I8_FUSED");
-        fused = e && e[0] == '1';
-    }
-    const int widen = int8 && !fused && d->rows >= QW_WIDEN_MIN_ROWS;
+     * without their in-loop widening. */
+    const int widen = int8 && d->rows >= QW_WIDEN_MIN_ROWS;
     const void *wptr = d->weight->ptr;
     if (widen) {
         const size_t n = (size_t)d->cols * d->k, bytes = n * 2;
@@ -986,40 +945,11 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
         a.a_bytes = (uint32_t)ab;
         a.w_bytes = (uint32_t)wb;
     }
-    /* kernel family: QW_GEMM_SHAPE = b (256 x 256, 8 waves, two
-     * per SIMD), a (256 x 256, 4 waves), r (128 x 256, 4 waves, two
-     * workgroups per CU) or d (default: b with 16x16x32 MFMAs, bf16 weights;
-     * in-loop int8 widening runs b's kernels) */
-    static char shape_env = 0;
-    if (!shape_env) {
-        const char *e = getenv("QW_GEMM_SHAPE");
-        shape_env = (e && e[0] && strchr("abdr", e[0])) ? e[0] : 'd';
-    }
-    const char shape = shape_env == 'd' && int8 && !widen ? 'b' : shape_env;
+    /* bf16 weights (or int8 widened above): the 16x16x32-MFMA kernels;
+     * int8 weights with few rows: the kernels that widen in their K loop */
     const int qkn = d->epilogue == QW_LINEAR_QKNORM;
-    /* the fused q/k epilogue exists for shapes b and d; a and r store and
-     * run the separate norm + rope kernel afterwards */
-    static int qkn_fused = -1;
-    if (qkn_fused < 0) {
-        const char *e = getenv("QW_QKN_FUSED");
-        qkn_fused = !(e && e[0] == '0');
-    }
-    const int qkn_after = qkn && (shape == 'a' || shape == 'r' || !qkn_fused);
-    int kid = (int8 && !widen ? K_GEMM_I8_STORE : K_GEMM_BF16_STORE) +
-              (qkn ? QW_LINEAR_STORE : d->epilogue);
-    unsigned threads = 256, bm = 256, bn = 256;
-    if (shape == 'b') {
-        kid += K_GEMM_BF16_STORE_W8 - K_GEMM_BF16_STORE;
-        threads = 512;
-        if (qkn && !qkn_after) kid = int8 && !widen ? K_GEMM_I8_QKN_W8 : K_GEMM_BF16_QKN_W8;
-    } else if (shape == 'd') { /* b's geometry with 16x16x32 MFMAs */
-        kid += K_GEMM_BF16_STORE_D - K_GEMM_BF16_STORE;
-        if (qkn && !qkn_after) kid = K_GEMM_BF16_QKN_D;
-        threads = 512;
-    } else if (shape == 'r') {
-        kid += K_GEMM_BF16_STORE_R - K_GEMM_BF16_STORE;
-        bm = 128;
-    }
+    const int kid = (int8 && !widen ? K_GEMM_I8_STORE_W8 : K_GEMM_BF16_STORE_D) + d->epilogue;
+    const unsigned threads = 512, bm = 256, bn = 256;
     a.norm_q = qkn ? (const uint16_t *)d->norm_q->ptr : NULL;
     a.norm_k = qkn ? (const uint16_t *)d->norm_k->ptr : NULL;
     a.rope_cos = qkn ? (const float *)d->rope_cos->ptr : NULL;
@@ -1035,7 +965,7 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     a.sk_part = NULL;
     a.sk_flag = NULL;
     uint32_t grid = tiles;
-    if (shape != 'r') {
+    {
         const uint32_t s = split_choice(g, tiles, d->k / 64);
         if (s > 1) {
             if (!g->sk_part) {
@@ -1061,25 +991,13 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
             grid = a.dp_tiles + R * s;
         }
     }
-    {
-        static int persist = -1;
-        if (persist < 0) {
-            const char *e = getenv("QW_GEMM_PERSIST");
-            persist = !(e && e[0] == '0');
-        }
-        /* shape d without split tiles: one workgroup per CU walks the tiles,
-         * so a tile's output stores drain under the next tile's first loads
-         * (up 521 -> 514 us, QKV 365 -> 359 us; QW_GEMM_PERSIST=0: one
-         * workgroup per tile) */
-        if (persist && shape == 'd' && a.split == 1 && grid > g->cus && g->cus % 8 == 0)
-            grid = g->cus;
-    }
-    if (!launch(g, kid, dim3(grid), dim3(threads), a)) return 0;
-    if (qkn_after)
-        return qw_gpu_qk_norm_rope_bf16(g, d->out, d->rows, d->cols / 384, d->ldc, d->cols / 3,
-                                        d->norm_q, d->norm_k, d->rope_cos, d->rope_sin,
-                                        d->rope_rows, d->eps);
-    return 1;
+    /* bf16-weight kernels without split tiles: one workgroup per CU walks
+     * the tiles, so a tile's output stores drain under the next tile's first
+     * loads (up 521 -> 514 us, QKV 365 -> 359 us against one workgroup per
+     * tile) */
+    if (kid >= K_GEMM_BF16_STORE_D && a.split == 1 && grid > g->cus && g->cus % 8 == 0)
+        grid = g->cus;
+    return launch(g, kid, dim3(grid), dim3(threads), a);
 }
 
 static qw_linear_desc plain_linear(h3_gpu_tensor *out, const h3_gpu_tensor *in,

@@ -73,13 +73,8 @@ __device__ __forceinline__ float attn_exp(const floatx16 (&s)[AKB], bf16x8 (&pf)
         const int kbk = tk >> 1, v0 = 8 * (tk & 1);
 #pragma unroll
         for (int u = 0; u < 8; u += 2) {
-#ifdef QW_EXP_ATT_NOEXP /* experiments only (like QW_EXP_ATT_NOK / NOV / FIXKV) */
-            const float p0 = __builtin_fmaf(s[kbk][v0 + u], c, -m_use);
-            const float p1 = __builtin_fmaf(s[kbk][v0 + u + 1], c, -m_use);
-#else
             const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kbk][v0 + u], c, -m_use));
             const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kbk][v0 + u + 1], c, -m_use));
-#endif
             const qw_b2 pp = __builtin_bit_cast(qw_b2, pack_bf(p0, p1));
             pf[tk][u] = pp[0];
             pf[tk][u + 1] = pp[1];
@@ -201,10 +196,6 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
     const uint32_t drow = lane >> 4, dphys = lane & 15;
     auto issue = [&](uint32_t kstage, uint32_t kv0k, uint32_t vstage, uint32_t kv0v)
         __attribute__((always_inline)) {
-#ifdef QW_EXP_ATT_FIXKV
-        kv0k = 0;
-        kv0v = 0;
-#endif
 #pragma unroll
         for (int jj = 0; jj < DPW; jj++) {
             const uint32_t blk = wave * DPW + jj;     /* 1 KB block of the tile */
@@ -228,12 +219,8 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
 #pragma unroll
                 for (int v = 0; v < 16; v++) s[kbk][v] = 0.0f;
             }
-#ifdef QW_EXP_ATT_NOK
-            const bf16x8 kf = qf[(st + 1) & 7];
-#else
             const bf16x8 kf = *(const bf16x8 *)(ks + (kbk * 32 + j) * 256 +
                                                 (((2 * st + h) ^ (j & 15)) << 4));
-#endif
             s[kbk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[st], s[kbk], 0, 0, 0);
         }
     };
@@ -257,11 +244,7 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
                     (attn_lds_b4 *)(vs + r0 * 256 + ((cc ^ (4 * (r0 & 3))) << 4) + half * 8));
                 const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
                     (attn_lds_b4 *)(vs + r1 * 256 + ((cc ^ (4 * (r1 & 3))) << 4) + half * 8));
-#ifdef QW_EXP_ATT_NOV
-                const bf16x8 vf = qf[(tk + db) & 7];
-#else
                 const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-#endif
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[tk], o[db], 0, 0, 0);
             }
         }

@@ -2,18 +2,16 @@
  *   out[m, n] = epilogue( sum_k A[m, k] * W[n, k] )
  * A bf16 row-major (row stride lda), W in the checkpoint's native [out, in]
  * layout (bf16, or int8 with one fp32 scale per output row), fp32
- * accumulation in v_mfma_f32_32x32x16_bf16 (or 16x16x32, shape D).
+ * accumulation on the matrix cores.
  *
  * Tiling (template): a workgroup of WM x WN waves computes a BM x BN tile,
  * BM = WM * MI * 32, BN = WN * NI * 32, each wave an (MI*32) x (NI*32) block
- * of MI x NI MFMA tiles, stepping K by 64. Shapes in use:
- *   A: 2 x 2 waves of 4 x 4 blocks (256 x 256, one wave per SIMD, 256
- *      accumulators per lane);
- *   B: 4 x 2 waves of 2 x 4 blocks (256 x 256, two waves per SIMD, 128
- *      accumulators each: one wave's MFMAs cover the other's LDS/global
- *      latency);
- *   D: B's geometry with each 32 x 32 block computed as four 16 x 16 blocks
- *      of v_mfma_f32_16x16x32_bf16 (the runtime's default for bf16 weights).
+ * of MI x NI MFMA tiles, stepping K by 64. One geometry is built: 4 x 2
+ * waves of 2 x 4 blocks (256 x 256, two waves per SIMD, 128 accumulators
+ * each: one wave's MFMAs cover the other's LDS/global latency). bf16
+ * weights use v_mfma_f32_16x16x32_bf16 (each 32 x 32 block as four 16 x 16
+ * blocks, the "_d" kernels); int8 weights widened in the loop use
+ * v_mfma_f32_32x32x16_bf16 (the "_w8" kernels).
  * A and W tiles are staged through LDS, double-buffered (2 x 64 KB at
  * 256 x 256), with the next K-slice's global loads in flight while the
  * current one is multiplied; within a K-slice the operand fragments of
@@ -26,10 +24,9 @@
  * per-row scale multiplies the fp32 sum in the epilogue, so the contraction
  * equals the dequantised product.
  *
- * The MFMA is issued as C^T = W A^T (W fragment as the A operand): each
- * lane then holds, for one output row, runs of 4 consecutive output
- * columns, stored as 8-byte writes with the epilogue (scale, bias, GELU,
- * residual gate) applied in registers.
+ * The MFMA is issued as C^T = W A^T (W fragment as the A operand). The
+ * epilogue (scale, bias, GELU, residual gate, q/k norm + RoPE) stages the
+ * fp32 sums through LDS and writes whole 256-byte row runs.
  */
 #pragma once
 #include "common.h"
@@ -44,13 +41,6 @@
 #define QW_SPLIT_PART (256u * 256u)
 /* buffer cache policy sc0 | sc1: coherent at device scope */
 #define QW_CPOL_COHERENT 17
-/* QW_EXP_FIXED_K (experiments only, never in the shipped build): every
- * K-slice load re-reads slice 0, isolating global-memory effects. */
-#ifdef QW_EXP_FIXED_K
-#define QW_K(x) 0
-#else
-#define QW_K(x) (x)
-#endif
 
 __device__ __forceinline__ uint32_t g_swz(uint32_t row, uint32_t chunk) {
     return row * 128u + ((chunk ^ ((row >> 1) & 7u)) << 4);
@@ -178,13 +168,6 @@ __device__ __forceinline__ void gemm_tile_at(const qw_gemm_args &a, uint32_t pid
 #ifndef QW_GEMM_GROUP
 #define QW_GEMM_GROUP 8
 #endif
-#ifdef QW_EXP_ROWMAJOR
-    if (a.tiles_n <= QW_EXP_ROWMAJOR) {
-        tm = pid / a.tiles_n;
-        tn = pid % a.tiles_n;
-        return;
-    }
-#endif
     const uint32_t G = QW_GEMM_GROUP;
     const uint32_t per_group = G * a.tiles_n;
     const uint32_t first_m = (pid / per_group) * G;
@@ -198,73 +181,6 @@ __device__ __forceinline__ void gemm_tile(const qw_gemm_args &a, uint32_t &tm, u
     uint32_t pid = blockIdx.x;
     if ((nt & 7u) == 0) pid = (pid & 7u) * (nt >> 3) + (pid >> 3);
     gemm_tile_at(a, pid, tm, tn);
-}
-
-/* Epilogue of one wave's (MI*32) x (NI*32) block of C^T accumulators:
- * acc[ni][mi][4g + j] = C[row, col] with row = row0 + mi*32 + i32 and
- * col = col0 + ni*32 + 8g + 4h + j. y = bf16(acc * wscale + bias), then
- * the epilogue op, written as 8-byte runs of 4 columns. */
-template <int EPI, int INT8, int MI, int NI>
-__device__ __forceinline__ void gemm_epilogue(const qw_gemm_args &a, floatx16 (&acc)[NI][MI],
-                                              uint32_t row0, uint32_t col0, uint32_t h,
-                                              uint32_t i32) {
-#pragma clang fp contract(off)
-    /* int8 weights, or bf16 weights widened from int8 by qw_widen_i8_bf16 */
-    const bool scaled = INT8 || a.wscale != nullptr;
-#ifdef QW_EXP_NO_EPI
-    { /* experiments only: keep the sums live, skip the epilogue */
-        float s = 0.0f;
-#pragma unroll
-        for (int ni = 0; ni < NI; ni++)
-#pragma unroll
-            for (int mi = 0; mi < MI; mi++) s += acc[ni][mi][0];
-        if (s != 1234.5f) return;
-    }
-#endif
-#pragma unroll
-    for (int ni = 0; ni < NI; ni++) {
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const uint32_t col = col0 + ni * 32 + 8 * g + 4 * h;
-            if (col >= a.n) continue; /* n % 8 == 0: a group is all in or out */
-            floatx4 sc = {1.0f, 1.0f, 1.0f, 1.0f};
-            if (scaled) sc = *(const floatx4 *)(a.wscale + col);
-            float bias[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (a.bias) {
-                const u32x2 bb = *(const u32x2 *)(a.bias + col);
-                bias[0] = lo_bf(bb[0]);
-                bias[1] = hi_bf(bb[0]);
-                bias[2] = lo_bf(bb[1]);
-                bias[3] = hi_bf(bb[1]);
-            }
-#pragma unroll
-            for (int mi = 0; mi < MI; mi++) {
-                const uint32_t row = row0 + mi * 32 + i32;
-                if (row >= a.m) continue;
-                float y[4];
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    float t = acc[ni][mi][4 * g + j];
-                    if (scaled) t *= sc[j];
-                    y[j] = bf2f(f2bf(t + bias[j]));
-                }
-                u16 *dst = a.out + (size_t)row * a.ldc + col;
-                if (EPI == QW_EPI_GELU) {
-#pragma unroll
-                    for (int j = 0; j < 4; j++) y[j] = gelu_tanh_f(y[j]);
-                } else if (EPI == QW_EPI_GATE) {
-                    const u32x2 gv =
-                        *(const u32x2 *)(a.gate + (size_t)a.row_map[row] * a.gate_row_stride + col);
-                    const u32x2 rv = *(const u32x2 *)dst;
-                    y[0] = lo_bf(rv[0]) + y[0] * lo_bf(gv[0]);
-                    y[1] = hi_bf(rv[0]) + y[1] * hi_bf(gv[0]);
-                    y[2] = lo_bf(rv[1]) + y[2] * lo_bf(gv[1]);
-                    y[3] = hi_bf(rv[1]) + y[3] * hi_bf(gv[1]);
-                }
-                *(u32x2 *)dst = u32x2{pack_bf(y[0], y[1]), pack_bf(y[2], y[3])};
-            }
-        }
-    }
 }
 
 /* Epilogue through LDS: the same arithmetic as gemm_epilogue, but the
@@ -443,9 +359,6 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx1
                     y[2 * j + 1] = hi_bf(rv[j]) + y[2 * j + 1] * hi_bf(gv[j]);
                 }
             }
-#ifdef QW_EXP_EPI_NOSTORE /* experiments only: everything but the store */
-            if (a.ldc != 0x7FFFFFFFu) continue;
-#endif
             /* non-temporal store: measured 3% faster on the up projection
              * and 8% on 8192^3 than a default-policy store */
             __builtin_nontemporal_store(u32x4{pack_bf(y[0], y[1]), pack_bf(y[2], y[3]),
@@ -721,9 +634,9 @@ __device__ __forceinline__ void gemm_pipe_slice16(const PipeCtx<A_DL, W_DL, WLD>
 }
 
 /* Sums of tile (tm, tn) over k-steps [kb, ke) (64 k each) into acc; the
- * PF == 1, 2 pipelines take the whole k range only. Ends with the LDS
+ * Ends with the LDS
  * stages free (after a barrier). */
-template <int INT8, int WM, int WN, int MI, int NI, int PF, int FDB, int MF = 32, bool SPREAD = false>
+template <int INT8, int WM, int WN, int MI, int NI, int MF = 32, bool SPREAD = false>
 __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned char *lds,
                                               unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                               uint32_t kb, uint32_t ke,
@@ -764,10 +677,8 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
         w_off[j] = (r * a.k + wc * (INT8 ? 16 : 8)) * WES;
     }
 
-    /* PF staging register sets: slice kt + PF is loaded while slice kt is
-     * multiplied (set index = slice % PF), then slice kt + 1 is written to
-     * the other LDS buffer; PF = 2 gives loads two slices to land */
-    u32x4 ra[PF > 0 ? PF : 1][S::A_LD], rw[PF > 0 ? PF : 1][WLD];
+    /* staging registers of the int8 W prologue (widened on the way into LDS) */
+    u32x4 ra[1][S::A_LD], rw[1][WLD];
 #define QW_LOAD(SET, k0)                                                                      \
     do {                                                                                       \
         _Pragma("unroll") for (int j = 0; j < S::A_LD; j++) ra[SET][j] = __builtin_bit_cast(   \
@@ -807,40 +718,9 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
      * term (row / 2) % 8 only depends on i32 (blocks are 32-aligned) */
     const uint32_t a_row0 = wm * (MI * 32) + i32, w_row0 = wn * (NI * 32) + i32;
     const uint32_t swz = (i32 >> 1) & 7u;
-#define QW_FRAG(row, ks) ((row) * 128u + (((2 * (ks) + h) ^ swz) << 4))
 
     const uint32_t KT = ke;
-#define QW_COMPUTE_AT(base)                                                                     \
-    do {                                                                                        \
-        const unsigned char *As = (base);                                                       \
-        const unsigned char *Ws = As + S::A_BYTES;                                              \
-        bf16x8 af[1 + FDB][MI], bw[1 + FDB][NI];                                                \
-        _Pragma("unroll") for (int i = 0; i < MI; i++) af[0][i] =                               \
-            *(const bf16x8 *)(As + QW_FRAG(a_row0 + 32 * i, 0));                                \
-        _Pragma("unroll") for (int i = 0; i < NI; i++) bw[0][i] =                               \
-            *(const bf16x8 *)(Ws + QW_FRAG(w_row0 + 32 * i, 0));                                \
-        _Pragma("unroll") for (uint32_t ks = 0; ks < 4; ks++) {                                 \
-            const int c = FDB ? (ks & 1) : 0;                                                   \
-            if (!FDB && ks > 0) {                                                               \
-                _Pragma("unroll") for (int i = 0; i < MI; i++) af[0][i] =                       \
-                    *(const bf16x8 *)(As + QW_FRAG(a_row0 + 32 * i, ks));                       \
-                _Pragma("unroll") for (int i = 0; i < NI; i++) bw[0][i] =                       \
-                    *(const bf16x8 *)(Ws + QW_FRAG(w_row0 + 32 * i, ks));                       \
-            }                                                                                   \
-            if (FDB && ks + 1 < 4) {                                                            \
-                _Pragma("unroll") for (int i = 0; i < MI; i++) af[c ^ FDB][i] =                 \
-                    *(const bf16x8 *)(As + QW_FRAG(a_row0 + 32 * i, ks + 1));                   \
-                _Pragma("unroll") for (int i = 0; i < NI; i++) bw[c ^ FDB][i] =                 \
-                    *(const bf16x8 *)(Ws + QW_FRAG(w_row0 + 32 * i, ks + 1));                   \
-            }                                                                                   \
-            _Pragma("unroll") for (int ni = 0; ni < NI; ni++)                                   \
-                _Pragma("unroll") for (int mi = 0; mi < MI; mi++) acc[ni][mi] =                 \
-                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[c][ni], af[c][mi], acc[ni][mi],  \
-                                                            0, 0, 0);                           \
-        }                                                                                       \
-    } while (0)
-#define QW_COMPUTE(cur) QW_COMPUTE_AT(lds + (cur) * S::STAGE)
-    if (PF == 0) {
+    {
         /* Direct-to-LDS pipeline. The A tile (and a bf16 W tile) are loaded
          * with buffer_load_dwordx4 ... lds: each instruction writes 1 KB
          * (8 rows) of a wave's share of the tile straight into LDS, lane l
@@ -903,7 +783,7 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
             {
                 const uint32_t nk = (kb + 1 < KT ? kb + 1 : kb) * GBK;
                 gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, false, SPREAD>(
-                    c, acc, pa, pw, lds, lds_b, QW_K(nk));
+                    c, acc, pa, pw, lds, lds_b, nk);
                 QW_SLICE_END();
             }
             /* two slices per trip, so each one's stages are fixed at compile
@@ -911,15 +791,15 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
             uint32_t kt = kb + 1;
             for (; kt + 1 < KT; kt += 2) {
                 gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true, SPREAD>(
-                    c, acc, pa, pw, lds_b, lds, QW_K((kt + 1) * GBK));
+                    c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
                 QW_SLICE_END();
                 gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true, SPREAD>(
-                    c, acc, pa, pw, lds, lds_b, QW_K((kt + 2 < KT ? kt + 2 : kt + 1) * GBK));
+                    c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
                 QW_SLICE_END();
             }
             if (kt < KT) { /* the last slice, from stage lds_b */
                 gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true, SPREAD>(
-                    c, acc, pa, pw, lds_b, lds, QW_K(kt * GBK));
+                    c, acc, pa, pw, lds_b, lds, kt * GBK);
                 QW_SLICE_END();
             }
     #pragma unroll
@@ -932,7 +812,7 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
             {
                 const uint32_t nk = (kb + 1 < KT ? kb + 1 : kb) * GBK;
                 gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, false>(
-                    c, acc, pa, pw, lds, lds_b, QW_K(nk));
+                    c, acc, pa, pw, lds, lds_b, nk);
                 __builtin_amdgcn_s_waitcnt(0x0F70);
                 __syncthreads();
             }
@@ -941,17 +821,17 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
             uint32_t kt = kb + 1;
             for (; kt + 1 < KT; kt += 2) {
                 gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
-                    c, acc, pa, pw, lds_b, lds, QW_K((kt + 1) * GBK));
+                    c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
                 __builtin_amdgcn_s_waitcnt(0x0F70);
                 __syncthreads();
                 gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
-                    c, acc, pa, pw, lds, lds_b, QW_K((kt + 2 < KT ? kt + 2 : kt + 1) * GBK));
+                    c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
                 __builtin_amdgcn_s_waitcnt(0x0F70);
                 __syncthreads();
             }
             if (kt < KT) { /* the last slice, from stage lds_b */
                 gemm_pipe_slice<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true>(
-                    c, acc, pa, pw, lds_b, lds, QW_K(kt * GBK));
+                    c, acc, pa, pw, lds_b, lds, kt * GBK);
                 __builtin_amdgcn_s_waitcnt(0x0F70);
                 __syncthreads();
             }
@@ -962,45 +842,14 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
                     acc[ni][mi] =
                         __builtin_amdgcn_mfma_f32_32x32x16_bf16(pw[ni], pa[mi], acc[ni][mi], 0, 0, 0);
         }
-    } else if (PF == 1) {
-        QW_LOAD(0, 0);
-        store_lds(ra[0], rw[0], 0);
-        __syncthreads();
-        for (uint32_t kt = 0; kt < KT; kt++) {
-            const uint32_t cur = kt & 1;
-            if (kt + 1 < KT) QW_LOAD(0, QW_K((kt + 1) * GBK));
-            QW_COMPUTE(cur);
-            if (kt + 1 < KT) store_lds(ra[0], rw[0], cur ^ 1);
-            __syncthreads();
-        }
-    } else {
-        /* slice j: register set j % 2, LDS buffer j % 2 */
-        QW_LOAD(0, 0);
-        if (KT > 1) QW_LOAD(PF - 1, QW_K(GBK));
-        store_lds(ra[0], rw[0], 0);
-        __syncthreads();
-        for (uint32_t kt = 0; kt < KT; kt += 2) {
-            if (kt + 2 < KT) QW_LOAD(0, QW_K((kt + 2) * GBK));
-            QW_COMPUTE(0);
-            if (kt + 1 < KT) store_lds(ra[PF - 1], rw[PF - 1], 1);
-            __syncthreads();
-            if (kt + 1 >= KT) break;
-            if (kt + 3 < KT) QW_LOAD(PF - 1, QW_K((kt + 3) * GBK));
-            QW_COMPUTE(1);
-            if (kt + 2 < KT) store_lds(ra[0], rw[0], 0);
-            __syncthreads();
-        }
     }
-#undef QW_COMPUTE
-#undef QW_COMPUTE_AT
 #undef QW_LOAD
-#undef QW_FRAG
 }
 
 /* Epilogue of a finished tile (bf16 output plus the EPI op), or with pst the
  * fp32 sums of one piece of a split tile, or with pld the sum of all its
  * pieces followed by the epilogue */
-template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int MF = 32>
+template <int EPI, int INT8, int WM, int WN, int MI, int NI, int MF = 32>
 __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char *lds,
                                             unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                             floatx16 (&acc)[NI][MI], float *pst = nullptr,
@@ -1012,8 +861,8 @@ __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char
     const uint32_t wm = wave / WN, wn = wave % WN;
     const uint32_t h = lane >> 5, i32 = lane & 31;
     const uint32_t row0 = tm * S::BM + wm * (MI * 32), col0 = tn * S::BN + wn * (NI * 32);
-#ifndef QW_EXP_NO_EPI
-    if (PF == 0 && NI == 4) {
+    static_assert(NI == 4, "the LDS epilogue maps 16 lanes to one 128-column row");
+    {
         /* the stages are free after the loop's last barrier: the first half
          * of the waves stage through `lds`, the second through `lds_b`, one
          * 32-row slab (16.5 KB) per wave at a time */
@@ -1025,19 +874,15 @@ __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char
         gemm_epilogue_lds<EPI, INT8, MI, NI, MF>(a, acc, region, row0, col0, h, i32, lane,
                                              pst ? pst + poff : nullptr, pld ? pld + poff : nullptr,
                                              npart, own);
-        return;
     }
-#endif
-    gemm_epilogue<EPI, INT8, MI, NI>(a, acc, row0, col0, h, i32);
 }
 
-template <int EPI, int INT8, int WM, int WN, int MI, int NI, int PF, int FDB, int MF = 32,
-          bool SPREAD = false>
+template <int EPI, int INT8, int WM, int WN, int MI, int NI, int MF = 32, bool SPREAD = false>
 __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned char *lds,
                                              unsigned char *lds_b) {
     const uint32_t KT = a.k / GBK;
     const uint32_t nt = a.tiles_m * a.tiles_n;
-    const bool split = PF == 0 && NI == 4 && a.split > 1;
+    const bool split = a.split > 1;
     const uint32_t ndp = split ? a.dp_tiles : nt;
     floatx16 acc[NI][MI]; /* C^T blocks */
     uint32_t pid = blockIdx.x, tm, tn;
@@ -1051,8 +896,8 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
                 uint32_t q = id;
                 if ((ndp & 7u) == 0) q = (q & 7u) * (ndp >> 3) + (q >> 3);
                 gemm_tile_at(a, q, tm, tn);
-                gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD>(a, lds, lds_b, tm, tn, 0, KT, acc);
-                gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc);
+                gemm_mainloop<INT8, WM, WN, MI, NI, MF, SPREAD>(a, lds, lds_b, tm, tn, 0, KT, acc);
+                gemm_finish<EPI, INT8, WM, WN, MI, NI, MF>(a, lds, lds_b, tm, tn, acc);
                 /* every wave's slab reads done before the next tile's loads
                  * land in the stages (stores may stay in flight) */
                 asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -1061,8 +906,8 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
         }
         if ((ndp & 7u) == 0) pid = (pid & 7u) * (ndp >> 3) + (pid >> 3);
         gemm_tile_at(a, pid, tm, tn);
-        gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD>(a, lds, lds_b, tm, tn, 0, KT, acc);
-        gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc);
+        gemm_mainloop<INT8, WM, WN, MI, NI, MF, SPREAD>(a, lds, lds_b, tm, tn, 0, KT, acc);
+        gemm_finish<EPI, INT8, WM, WN, MI, NI, MF>(a, lds, lds_b, tm, tn, acc);
         return;
     }
     /* Piece of a split tile. Pieces are numbered k-range-major, so the
@@ -1075,9 +920,9 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     const uint32_t piece = q / R, r = q % R;
     const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
     gemm_tile_at(a, ndp + r, tm, tn);
-    gemm_mainloop<INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD>(a, lds, lds_b, tm, tn, kb, ke, acc);
+    gemm_mainloop<INT8, WM, WN, MI, NI, MF, SPREAD>(a, lds, lds_b, tm, tn, kb, ke, acc);
     float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
-    gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc,
+    gemm_finish<EPI, INT8, WM, WN, MI, NI, MF>(a, lds, lds_b, tm, tn, acc,
                                                slots + (size_t)piece * QW_SPLIT_PART);
     /* publish the partial (its coherent stores complete before the
      * workgroup's barrier), then count it. Agent-scope release/acquire
@@ -1093,7 +938,7 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     if (ticket != S - 1) return;
     /* last piece in: the others' partials are read with coherent loads */
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    gemm_finish<EPI, INT8, WM, WN, MI, NI, PF, MF>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S,
+    gemm_finish<EPI, INT8, WM, WN, MI, NI, MF>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S,
                                                piece);
     if (threadIdx.x == 0)
         __hip_atomic_store(a.sk_flag + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1108,49 +953,24 @@ struct GemmLds {
     static constexpr int BYTES = STAGE > SLABS ? STAGE : SLABS;
 };
 
-#define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI, PF, FDB) \
-    QW_GEMM_ENTRY_MF(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, 32)
-#define QW_GEMM_ENTRY_MF(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, MF) \
-    QW_GEMM_ENTRY_SP(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, MF, false)
-#define QW_GEMM_ENTRY_SP(name, EPI, INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD)                  \
+#define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI, MF, SPREAD)                           \
     QW_KERNEL void __launch_bounds__(64 * WM * WN, 1) name(qw_gemm_args a) {                 \
-        __shared__ __attribute__((aligned(16))) unsigned char                                \
-            lds[PF == 0 ? GemmLds<WM, WN, MI, NI>::BYTES : 2 * GemmShape<WM, WN, MI, NI>::STAGE]; \
-        __shared__ __attribute__((aligned(16)))                                               \
-            unsigned char lds_b[PF == 0 ? GemmLds<WM, WN, MI, NI>::BYTES : 16];              \
-        qw_gemm_impl<EPI, INT8, WM, WN, MI, NI, PF, FDB, MF, SPREAD>(a, lds, lds_b);              \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[GemmLds<WM, WN, MI, NI>::BYTES]; \
+        __shared__ __attribute__((aligned(16))) unsigned char lds_b[GemmLds<WM, WN, MI, NI>::BYTES]; \
+        qw_gemm_impl<EPI, INT8, WM, WN, MI, NI, MF, SPREAD>(a, lds, lds_b);                  \
     }
 
-/* shape A: 4 waves, 128 x 128 per wave */
-#ifndef QW_A_PF
-#define QW_A_PF 0
-#endif
-QW_GEMM_ENTRY(qw_gemm_bf16_store, QW_EPI_STORE, 0, 2, 2, 4, 4, QW_A_PF, 1)
-QW_GEMM_ENTRY(qw_gemm_bf16_gelu, QW_EPI_GELU, 0, 2, 2, 4, 4, QW_A_PF, 1)
-QW_GEMM_ENTRY(qw_gemm_bf16_gate, QW_EPI_GATE, 0, 2, 2, 4, 4, QW_A_PF, 1)
-QW_GEMM_ENTRY(qw_gemm_i8_store, QW_EPI_STORE, 1, 2, 2, 4, 4, QW_A_PF, 1)
-QW_GEMM_ENTRY(qw_gemm_i8_gelu, QW_EPI_GELU, 1, 2, 2, 4, 4, QW_A_PF, 1)
-QW_GEMM_ENTRY(qw_gemm_i8_gate, QW_EPI_GATE, 1, 2, 2, 4, 4, QW_A_PF, 1)
-/* shape B: 8 waves (two per SIMD), 64 x 128 per wave */
-#ifndef QW_W8_PF
-#define QW_W8_PF 0
-#endif
-#ifndef QW_W8_FDB
-#define QW_W8_FDB 1
-#endif
-QW_GEMM_ENTRY(qw_gemm_bf16_store_w8, QW_EPI_STORE, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
-QW_GEMM_ENTRY(qw_gemm_bf16_gelu_w8, QW_EPI_GELU, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
-QW_GEMM_ENTRY(qw_gemm_bf16_gate_w8, QW_EPI_GATE, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
-QW_GEMM_ENTRY(qw_gemm_i8_store_w8, QW_EPI_STORE, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
-QW_GEMM_ENTRY(qw_gemm_i8_gelu_w8, QW_EPI_GELU, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
-QW_GEMM_ENTRY(qw_gemm_i8_gate_w8, QW_EPI_GATE, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
-QW_GEMM_ENTRY(qw_gemm_bf16_qkn_w8, QW_EPI_QKNORM, 0, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
-QW_GEMM_ENTRY(qw_gemm_i8_qkn_w8, QW_EPI_QKNORM, 1, 4, 2, 2, 4, QW_W8_PF, QW_W8_FDB)
-/* shape d (default): the geometry of b (8 waves of 64 x 128) with
- * v_mfma_f32_16x16x32_bf16, bf16 weights (int8 weights widened first); the
- * in-loop-widening int8 kernels are b's. (The same MFMA with a's geometry,
- * 4 waves of 128 x 128, measured 20-30% slower than b and is not built.) */
-QW_GEMM_ENTRY_MF(qw_gemm_bf16_store_d, QW_EPI_STORE, 0, 4, 2, 2, 4, 0, 1, 16)
-QW_GEMM_ENTRY_SP(qw_gemm_bf16_gelu_d, QW_EPI_GELU, 0, 4, 2, 2, 4, 0, 1, 16, true)
-QW_GEMM_ENTRY_SP(qw_gemm_bf16_gate_d, QW_EPI_GATE, 0, 4, 2, 2, 4, 0, 1, 16, true)
-QW_GEMM_ENTRY_MF(qw_gemm_bf16_qkn_d, QW_EPI_QKNORM, 0, 4, 2, 2, 4, 0, 1, 16)
+/* int8 weights widened in the K loop (linears of fewer than 512 rows, where
+ * a separate widening pass would not amortise): 8 waves (two per SIMD) of
+ * 64 x 128 with v_mfma_f32_32x32x16_bf16 */
+QW_GEMM_ENTRY(qw_gemm_i8_store_w8, QW_EPI_STORE, 1, 4, 2, 2, 4, 32, false)
+QW_GEMM_ENTRY(qw_gemm_i8_gelu_w8, QW_EPI_GELU, 1, 4, 2, 2, 4, 32, false)
+QW_GEMM_ENTRY(qw_gemm_i8_gate_w8, QW_EPI_GATE, 1, 4, 2, 2, 4, 32, false)
+QW_GEMM_ENTRY(qw_gemm_i8_qkn_w8, QW_EPI_QKNORM, 1, 4, 2, 2, 4, 32, false)
+/* bf16 weights (and int8 weights widened first): the same geometry with
+ * each 32 x 32 block computed as four 16 x 16 blocks of
+ * v_mfma_f32_16x16x32_bf16 */
+QW_GEMM_ENTRY(qw_gemm_bf16_store_d, QW_EPI_STORE, 0, 4, 2, 2, 4, 16, false)
+QW_GEMM_ENTRY(qw_gemm_bf16_gelu_d, QW_EPI_GELU, 0, 4, 2, 2, 4, 16, true)
+QW_GEMM_ENTRY(qw_gemm_bf16_gate_d, QW_EPI_GATE, 0, 4, 2, 2, 4, 16, true)
+QW_GEMM_ENTRY(qw_gemm_bf16_qkn_d, QW_EPI_QKNORM, 0, 4, 2, 2, 4, 16, false)

@@ -73,6 +73,13 @@ struct qw_dit {
     } lora[QW_DIT_MAX_LORA];
     int n_lora;
     h3_gpu_tensor **lora_base;
+    /* non-owning q / k / v row views of each layer's fused qkv weight (and
+     * of its int8 row scales), made on first request and remade when the
+     * live weight changes (LoRA fusion swaps it) */
+    struct qw_qkv_views {
+        const h3_gpu_tensor *src_w, *src_s;
+        h3_gpu_tensor *w[3], *s[3];
+    } *qkv_views;
     /* ti2i cross-step caches (slot 0: guided branch, 1: CFG negative) */
     struct qw_ti2i_cache {
         uint32_t rows, target_rows, seg_count;
@@ -459,7 +466,10 @@ static qw_lin *layer_lin(qw_layer *L, int j) {
 
 /* every adapter dropped, base weights back in the layers, fused copies and
  * ti2i caches (made with the old weights) freed */
+static void qkv_views_free(qw_dit *d);
+
 static void lora_reset(qw_dit *d) {
+    qkv_views_free(d);
     if (d->lora_base) {
         for (uint32_t l = 0; l < d->cfg.layers; l++)
             for (int j = 0; j < 4; j++) {
@@ -511,6 +521,7 @@ static int lora_matrix(qw_dit *d, const h3_st_header *h, const char *key, uint32
  * of apply / remove / scale changes does not matter and nothing rounds
  * twice). On failure the adapter state is reset to none. */
 static int lora_rebuild(qw_dit *d, char *error, size_t error_size) {
+    qkv_views_free(d);
     h3_gpu *g = d->gpu;
     int ok = 1;
     if (!d->lora_base) {
@@ -705,6 +716,7 @@ void qw_dit_free(qw_dit *d) {
             h3_gpu_tensor_free(d->layer[l].norm_k);
         }
     free(d->layer);
+    qkv_views_free(d);
     lin_free(&d->img_in);
     lin_free(&d->txt_in1);
     lin_free(&d->txt_in2);
@@ -722,11 +734,54 @@ void qw_dit_free(qw_dit *d) {
     free(d);
 }
 
+/* View of rows [part H, (part + 1) H) of the fused qkv weight (scales: 0)
+ * or of its row scales (scales: 1), rebuilt if the live tensor changed. */
+static const h3_gpu_tensor *qkv_part(qw_dit *d, int block, int part, int scales) {
+    const uint32_t H = d->cfg.hidden;
+    const qw_layer *L = &d->layer[block];
+    const h3_gpu_tensor *src = scales ? L->qkv.scales : L->qkv.w;
+    if (!src) return NULL;
+    if (!d->qkv_views) {
+        d->qkv_views = calloc(d->cfg.layers, sizeof(*d->qkv_views));
+        if (!d->qkv_views) return NULL;
+    }
+    struct qw_qkv_views *v = &d->qkv_views[block];
+    const h3_gpu_tensor **have = scales ? &v->src_s : &v->src_w;
+    h3_gpu_tensor **views = scales ? v->s : v->w;
+    if (*have != src) {
+        for (int i = 0; i < 3; i++) {
+            h3_gpu_tensor_free(views[i]);
+            views[i] = NULL;
+        }
+        *have = src;
+    }
+    if (!views[part]) {
+        const size_t per = scales ? H : (size_t)H * L->qkv.k;
+        views[part] = h3_gpu_tensor_view(src, per * (size_t)part, per);
+    }
+    return views[part];
+}
+
+static void qkv_views_free(qw_dit *d) {
+    if (!d->qkv_views) return;
+    for (uint32_t l = 0; l < d->cfg.layers; l++)
+        for (int i = 0; i < 3; i++) {
+            h3_gpu_tensor_free(d->qkv_views[l].w[i]);
+            h3_gpu_tensor_free(d->qkv_views[l].s[i]);
+        }
+    free(d->qkv_views);
+    d->qkv_views = NULL;
+}
+
+/* Fields as reference qwen_dit.h:84-86: 0 = to_q, 1 = to_k, 2 = to_v (row
+ * views of the fused [3H, H] weight), 3 = to_out, 4 = fc1, 5 = fc2. The
+ * views belong to the model (valid until the next LoRA change or
+ * qw_dit_free); the caller frees nothing. */
 const h3_gpu_tensor *qw_dit_block_tensor(const qw_dit *d, int block, int field) {
     if (!d || block < 0 || (uint32_t)block >= d->cfg.layers) return NULL;
     const qw_layer *L = &d->layer[block];
     switch (field) {
-    case 0: case 1: case 2: return L->qkv.w;
+    case 0: case 1: case 2: return qkv_part((qw_dit *)d, block, field, 0);
     case 3: return L->out.w;
     case 4: return L->fc1.w;
     case 5: return L->fc2.w;
@@ -738,7 +793,7 @@ const h3_gpu_tensor *qw_dit_block_scales(const qw_dit *d, int block, int field) 
     if (!d || block < 0 || (uint32_t)block >= d->cfg.layers) return NULL;
     const qw_layer *L = &d->layer[block];
     switch (field) {
-    case 0: case 1: case 2: return L->qkv.scales;
+    case 0: case 1: case 2: return qkv_part((qw_dit *)d, block, field, 1);
     case 3: return L->out.scales;
     case 4: return L->fc1.scales;
     case 5: return L->fc2.scales;

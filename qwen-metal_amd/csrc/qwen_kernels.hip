@@ -3,6 +3,5 @@
 #include "kernels/common.h"
 #include "kernels/elementwise.h"
 #include "kernels/gemm.h"
-#include "kernels/gemm_ring.h"
 #include "kernels/attention.h"
 #include "kernels/lora.h"

@@ -20,58 +20,71 @@ void qw_sched_cfg_default(qw_sched_cfg *c) {
     c->shift_terminal = 0.02;
 }
 
-static float f32(double v) { return (float)v; }
+/* FlowMatch sigma schedule (semantics of reference qwen_pipeline.m:130-205).
+ *
+ * Each step's timestep t_i (linear from 1 down to 1/steps, or the caller's
+ * turbo list) is a float32. With dynamic shifting it maps to
+ *     sigma_i = e^mu / (e^mu + (1 / t_i - 1)),
+ * mu = slope * seq_len + intercept on the line through (base_seq,
+ * base_shift) and (max_seq, max_shift), e^mu in double; 1 / t_i is taken
+ * in double and rounded to float32, the "- 1" is a float32 subtraction and
+ * the quotient is rounded to float32. The optional terminal stretch then
+ * rescales every 1 - sigma_i so the last sigma lands on shift_terminal:
+ *     k = fl32(fl32(1 - sigma_last) / (1 - shift_terminal)),
+ *     sigma_i = fl32(1 - fl32(1 - sigma_i) / k).
+ * Every listed fl32 is a rounding point of the released schedule; the
+ * float32 values are exact in the double output, which ends with 0. */
+static float fl32(double v) { return (float)v; }
+
+static double shift_exp_mu(const qw_sched_cfg *c, uint32_t seq_len) {
+    const double slope = c->max_seq == c->base_seq
+                             ? 0.0
+                             : (c->max_shift - c->base_shift) / (c->max_seq - c->base_seq);
+    const double intercept = c->base_shift - slope * c->base_seq;
+    return exp(slope * (double)seq_len + intercept);
+}
+
+static float base_timestep(uint32_t i, uint32_t steps, const double *turbo) {
+    if (turbo) return fl32(turbo[i]);
+    if (steps == 1) return 1.0f;
+    const double stride = (1.0 / steps - 1.0) / (double)(steps - 1);
+    return fl32(1.0 + (double)i * stride);
+}
 
 int qw_pipe_schedule(uint32_t steps, uint32_t seq_len, const double *turbo_sigmas,
                      uint32_t turbo_count, const qw_sched_cfg *cfg, double *sigmas_out,
                      char *error, size_t error_size) {
-    /* qwen_pipeline.m:130-205: float32 intermediates, exp(mu) in double. */
-    if (!steps || !seq_len || !sigmas_out || !cfg || steps > 1000) {
-        snprintf(error, error_size, "schedule: bad arguments");
+    if (!cfg || !sigmas_out || steps == 0 || seq_len == 0) {
+        snprintf(error, error_size, "qw_pipe_schedule: need a config, an output array, "
+                 "steps > 0 and seq_len > 0");
         return 0;
     }
     if (turbo_sigmas && turbo_count != steps) {
-        snprintf(error, error_size, "schedule: turbo sigmas %u != steps %u", turbo_count, steps);
+        snprintf(error, error_size,
+                 "qw_pipe_schedule: %u turbo timesteps given for a %u-step schedule",
+                 turbo_count, steps);
         return 0;
     }
-    double exp_mu = 0.0;
-    if (cfg->dynamic_shifting) {
-        double m = cfg->max_seq != cfg->base_seq
-                       ? (cfg->max_shift - cfg->base_shift) / (cfg->max_seq - cfg->base_seq)
-                       : 0.0;
-        double b = cfg->base_shift - m * cfg->base_seq;
-        exp_mu = exp((double)seq_len * m + b);
-    }
-    float *sh = malloc(sizeof(float) * steps);
-    if (!sh) {
-        snprintf(error, error_size, "schedule: out of memory");
-        return 0;
-    }
+    const double e_mu = cfg->dynamic_shifting ? shift_exp_mu(cfg, seq_len) : 0.0;
     for (uint32_t i = 0; i < steps; i++) {
-        double raw = turbo_sigmas ? turbo_sigmas[i]
-                     : steps == 1 ? 1.0
-                                  : 1.0 + (double)i * ((1.0 / steps) - 1.0) / (double)(steps - 1);
-        float t = f32(raw);
+        const float t = base_timestep(i, steps, turbo_sigmas);
+        float sigma = t;
         if (cfg->dynamic_shifting) {
-            float inv = f32(1.0 / t);
-            float base = f32(inv - 1.0f);
-            sh[i] = f32(exp_mu / (exp_mu + (double)base));
-        } else {
-            sh[i] = f32(raw);
+            const float odds = fl32(1.0 / t) - 1.0f;
+            sigma = fl32(e_mu / (e_mu + (double)odds));
         }
+        sigmas_out[i] = sigma;
     }
     if (cfg->has_terminal && cfg->shift_terminal < 1.0) {
-        float tail = f32(1.0 - (double)sh[steps - 1]);
-        float scale = f32((double)tail / (1.0 - cfg->shift_terminal));
-        if (scale != 0.0f)
+        const float k =
+            fl32((double)fl32(1.0 - sigmas_out[steps - 1]) / (1.0 - cfg->shift_terminal));
+        if (k != 0.0f)
             for (uint32_t i = 0; i < steps; i++) {
-                float om = f32(1.0 - (double)sh[i]);
-                sh[i] = f32(1.0 - (double)om / (double)scale);
+                const float rest = fl32(1.0 - sigmas_out[i]);
+                sigmas_out[i] = fl32(1.0 - (double)rest / (double)k);
             }
     }
-    for (uint32_t i = 0; i < steps; i++) sigmas_out[i] = sh[i];
     sigmas_out[steps] = 0.0;
-    free(sh);
     return 1;
 }
 
@@ -106,7 +119,7 @@ int qw_pipe_rope_tables(h3_gpu *gpu, uint32_t text_rows, uint32_t gh, uint32_t g
                         h3_gpu_tensor **rope_cos, h3_gpu_tensor **rope_sin, char *error,
                         size_t error_size) {
     if (!gh || !gw || !rope_cos || !rope_sin) {
-        snprintf(error, error_size, "rope: bad arguments");
+        snprintf(error, error_size, "qw_pipe_rope_tables: need gh, gw > 0 and two outputs");
         return 0;
     }
     const size_t n = (size_t)(text_rows + gh * gw) * 64;
@@ -124,7 +137,7 @@ int qw_pipe_rope_tables(h3_gpu *gpu, uint32_t text_rows, uint32_t gh, uint32_t g
     if (!ok) {
         h3_gpu_tensor_free(ct);
         h3_gpu_tensor_free(st);
-        snprintf(error, error_size, "rope: table build failed");
+        snprintf(error, error_size, "qw_pipe_rope_tables: host or device allocation failed");
         return 0;
     }
     *rope_cos = ct;

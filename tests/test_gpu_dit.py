@@ -378,15 +378,20 @@ def test_int8_weights_bit_exact(gpu, qd, oracle):
     import ctypes as C
     for layer in range(c["layers"]):
         L = om.m.layer[layer]
-        for field, lin in ((0, L.qkv), (3, L.out), (4, L.fc1), (5, L.fc2)):
-            n, k = lin.n, lin.k
+        # fields 0-2 (to_q, to_k, to_v) are row thirds of the fused qkv weight
+        for field, lin, part in ((0, L.qkv, 0), (1, L.qkv, 1), (2, L.qkv, 2), (3, L.out, None),
+                                 (4, L.fc1, None), (5, L.fc2, None)):
+            n_all, k = lin.n, lin.k
+            q_ref = np.ctypeslib.as_array(C.cast(lin.q, C.POINTER(C.c_int8)), (n_all * k,))
+            s_ref = np.ctypeslib.as_array(lin.scales, (n_all,))
+            n = n_all if part is None else n_all // 3
+            r0 = 0 if part is None else part * n
+            assert qd.lib().h3_gpu_tensor_elements(dit.block_tensor(layer, field)) == n * k
             wt = qd.Tensor(gpu, dit.block_tensor(layer, field), n * k, qd.I8, owner=dit)
             st = qd.Tensor(gpu, qd.lib().qw_dit_block_scales(dit.h, layer, field), n, qd.F32,
                            owner=dit)
-            q_ref = np.ctypeslib.as_array(C.cast(lin.q, C.POINTER(C.c_int8)), (n * k,))
-            s_ref = np.ctypeslib.as_array(lin.scales, (n,))
-            assert np.array_equal(wt.read(), q_ref)
-            assert np.array_equal(st.read(), s_ref)
+            assert np.array_equal(wt.read(), q_ref[r0 * k:(r0 + n) * k])
+            assert np.array_equal(st.read(), s_ref[r0:r0 + n])
             wt.h = st.h = None  # borrowed handles
     om.close()
     dit.close()
@@ -514,10 +519,17 @@ def test_lora_fusion_stack(gpu, qd, oracle, tmp_path):
         out = {}
         for l in range(c["layers"]):
             for j, (fid, rows, cols, _) in fields.items():
-                buf = np.empty(rows * cols, np.uint16)
-                assert L.h3_gpu_tensor_read_bf16(L.qw_dit_block_tensor(dit.h, l, fid),
-                                                 buf.ctypes.data, buf.size)
-                out[(l, j)] = buf.reshape(rows, cols)
+                # the fused qkv weight is read back through its to_q / to_k /
+                # to_v fields (0, 1, 2: [H, H] row views, reference order)
+                parts = (0, 1, 2) if fid == 0 else (fid,)
+                bufs = []
+                for f in parts:
+                    t = L.qw_dit_block_tensor(dit.h, l, f)
+                    buf = np.empty(rows * cols // len(parts), np.uint16)
+                    assert L.h3_gpu_tensor_elements(t) == buf.size
+                    assert L.h3_gpu_tensor_read_bf16(t, buf.ctypes.data, buf.size)
+                    bufs.append(buf)
+                out[(l, j)] = np.concatenate(bufs).reshape(rows, cols)
         return out
 
     def expect(base, stack):
