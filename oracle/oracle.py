@@ -113,6 +113,8 @@ def lib():
         L.qo_swiglu.argtypes = [u16p, u16p, SZ, SZ]
         L.qo_attention.argtypes = [u16p, SZ, u16p, SZ, u16p, SZ, u16p, SZ,
                                    u32p, SZ, SZ, SZ, SZ, C.c_float]
+        L.qo_attention_ex.argtypes = L.qo_attention.argtypes + [SZ]
+        L.qo_set_attention_p_mode.argtypes = [C.c_int]
         L.qo_t2i_limits.argtypes = [u32p, C.c_uint32, C.c_uint32, C.c_int]
         L.qo_modulation_reorder.argtypes = [u16p, u16p, SZ, SZ, C.c_int]
         L.qo_model_init_random.restype = C.c_int
@@ -190,14 +192,22 @@ def quantize_int8_rows(w, rows, cols):
 
 
 def attention(q, k, v, limits, q_rows, kv_rows, heads, head_dim=128,
-              scale=None, ldq=None, ldk=None, ldv=None):
+              scale=None, ldq=None, ldk=None, ldv=None, prescale_rows=0):
+    """prescale_rows: leading rows under the t2i text-row rule (q scaled and
+    re-rounded to bf16 before QK, h3_shaders.metal:4397-4401)"""
     hd = heads * head_dim
     scale = 1.0 / np.sqrt(head_dim) if scale is None else scale
     out = np.zeros((q_rows, hd), np.uint16)
-    lib().qo_attention(out, hd, q, ldq or hd, k, ldk or hd, v, ldv or hd,
-                       np.ascontiguousarray(limits, dtype=np.uint32), q_rows,
-                       kv_rows, heads, head_dim, float(scale))
+    lib().qo_attention_ex(out, hd, q, ldq or hd, k, ldk or hd, v, ldv or hd,
+                          np.ascontiguousarray(limits, dtype=np.uint32), q_rows,
+                          kv_rows, heads, head_dim, float(scale), prescale_rows)
     return out
+
+
+def set_attention_p_mode(mode):
+    """1: the oracle rounds each softmax probability to bf16 (as the flash
+    kernel's P operand), 0: fp32 probabilities"""
+    lib().qo_set_attention_p_mode(int(mode))
 
 
 def t2i_limits(rows, text_rows, text_causal):

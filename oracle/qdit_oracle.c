@@ -624,8 +624,20 @@ void qo_attention(uint16_t *out, size_t ldo, const uint16_t *q, size_t ldq,
                   const uint16_t *k, size_t ldk, const uint16_t *v, size_t ldv,
                   const uint32_t *limits, size_t q_rows, size_t kv_rows,
                   size_t heads, size_t head_dim, float scale) {
+    qo_attention_ex(out, ldo, q, ldq, k, ldk, v, ldv, limits, q_rows, kv_rows,
+                    heads, head_dim, scale, 0);
+}
+
+void qo_attention_ex(uint16_t *out, size_t ldo, const uint16_t *q, size_t ldq,
+                     const uint16_t *k, size_t ldk, const uint16_t *v, size_t ldv,
+                     const uint32_t *limits, size_t q_rows, size_t kv_rows,
+                     size_t heads, size_t head_dim, float scale,
+                     size_t prescale_rows) {
     /* tests/test_prefix_kernel.c:72-97: for each row, softmax over keys
-     * [0, limit) of (q.k) * scale in fp32, times V; one bf16 rounding. */
+     * [0, limit) of (q.k) * scale in fp32, times V; one bf16 rounding.
+     * Rows below prescale_rows follow h3_shaders.metal:4397-4401 (the t2i
+     * text rows): q is multiplied by the scale and re-rounded to bf16
+     * before the contraction, and the scores are not scaled again. */
     const size_t QB = 48;
     size_t D = head_dim;
     float *kf = malloc(sizeof(float) * heads * kv_rows * D);
@@ -655,8 +667,10 @@ void qo_attention(uint16_t *out, size_t ldo, const uint16_t *q, size_t ldq,
                     if (l > lmax) lmax = l;
                 }
                 for (size_t i = 0; i < nr; i++)
-                    for (size_t d = 0; d < D; d++)
-                        qf[i * D + d] = bf(q[(r0 + i) * ldq + h * D + d]);
+                    for (size_t d = 0; d < D; d++) {
+                        const float x = bf(q[(r0 + i) * ldq + h * D + d]);
+                        qf[i * D + d] = r0 + i < prescale_rows ? bf(rne(x * scale)) : x;
+                    }
                 gemm_nt_serial(qf, D, kf + h * kv_rows * D, D, s, kv_rows, nr,
                                lmax, D);
                 for (size_t i = 0; i < nr; i++) {
@@ -664,8 +678,9 @@ void qo_attention(uint16_t *out, size_t ldo, const uint16_t *q, size_t ldq,
                     if (l > kv_rows) l = (uint32_t)kv_rows;
                     float *row = s + i * kv_rows;
                     float m = -3.402823466e+38f;
+                    const float sc = r0 + i < prescale_rows ? 1.0f : scale;
                     for (uint32_t j = 0; j < l; j++) {
-                        row[j] *= scale;
+                        row[j] *= sc;
                         if (row[j] > m) m = row[j];
                     }
                     float denom = 0.0f;
@@ -920,8 +935,11 @@ void qo_block(const qo_model *m, int layer, uint16_t *hidden,
     qo_head_rms_norm(qkv + H, 3 * H, L->norm_k, rows, heads, 128, 1e-6f);
     qo_qk_rope(qkv, 3 * H, rope_cos, rope_sin, rows, heads, 128);
     qo_qk_rope(qkv + H, 3 * H, rope_cos, rope_sin, rows, heads, 128);
-    qo_attention(attn, H, qkv, 3 * H, qkv + H, 3 * H, qkv + 2 * H, 3 * H, lim,
-                 rows, rows, heads, 128, 1.0f / sqrtf(128.0f));
+    /* t2i: text rows pre-scale q (h3_shaders.metal:4397-4401); ti2i prefix
+     * tables run every row through the flash prefix kernel, which does not */
+    qo_attention_ex(attn, H, qkv, 3 * H, qkv + H, 3 * H, qkv + 2 * H, 3 * H, lim,
+                    rows, rows, heads, 128, 1.0f / sqrtf(128.0f),
+                    limits ? 0 : text_rows);
     if (debug_attn) memcpy(debug_attn, attn, sizeof(uint16_t) * rows * H);
     qo_apply_linear(&L->out, branch, H, attn, H, rows);
     qo_gate(hidden, hidden, branch, modulation, row_map, rows, H, slots, 2);

@@ -33,9 +33,18 @@
  *   gelu / silu / swiglu ........ textbook values at known points
  *   int8 quantizer .............. closed form (max row -> +-127, ties even)
  *   modulation reorder .......... dit_fixture modulation layout (slots)
- *   block / forward ............. composition of the above; no weights-free
- *                                 fixture exists: parity unpinned beyond
- *                                 its parts (the real checkpoint is absent)
+ *   embed / conditioning / block / final / forward / ti2i forward
+ *                                 structured weights reduce each stage to
+ *                                 a float64 closed form (q = k = 0 gives
+ *                                 uniform attention, identity and scaled
+ *                                 identity linears, distinct slot values),
+ *                                 zero gates give the identity, masking
+ *                                 invariants, forward = the reference's
+ *                                 composition bit for bit
+ *                                 (tests/test_oracle_composition.py; each
+ *                                 check fails under a swapped slot, a
+ *                                 misplaced shift or activation, a wrong
+ *                                 row_map, mask or feature row)
  */
 #ifndef QDIT_ORACLE_H
 #define QDIT_ORACLE_H
@@ -155,6 +164,13 @@ void qo_attention(uint16_t *out, size_t ldo, const uint16_t *q, size_t ldq,
                   const uint16_t *k, size_t ldk, const uint16_t *v, size_t ldv,
                   const uint32_t *limits, size_t q_rows, size_t kv_rows,
                   size_t heads, size_t head_dim, float scale);
+/* The same with the t2i text-row rule (h3_shaders.metal:4397-4401): rows
+ * below prescale_rows contract bf16(q * scale) with K, unscaled after. */
+void qo_attention_ex(uint16_t *out, size_t ldo, const uint16_t *q, size_t ldq,
+                     const uint16_t *k, size_t ldk, const uint16_t *v, size_t ldv,
+                     const uint32_t *limits, size_t q_rows, size_t kv_rows,
+                     size_t heads, size_t head_dim, float scale,
+                     size_t prescale_rows);
 /* qwen_dit.m:1651-1665 (t2i form): text rows causal (or full text prefix),
  * image rows see every key. */
 void qo_t2i_limits(uint32_t *limits, uint32_t rows, uint32_t text_rows,

@@ -1104,6 +1104,7 @@ extern "C" int qw_gpu_attention_bf16(h3_gpu *g, const qw_attention_desc *d) {
     a.ldo = d->ldo;
     a.text_rows = d->text_rows;
     a.text_causal = d->text_causal;
+    a.scale = d->scale;
     a.scale_log2 = d->scale * 1.4426950408889634f;
     g->stats.mps_sdpa_dispatches += 0;
     if (((uint64_t)(d->kv_rows - 1) * std::max(d->ldk, d->ldv) + hd) * 2 >= (1ull << 31))

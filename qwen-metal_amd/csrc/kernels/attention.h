@@ -23,7 +23,7 @@
  * arithmetic or LDS write instruction touches the operands.
  *
  * Softmax runs in fp32 in the log2 domain (scale * log2 e folded into one
- * FMA before exp2); P is rounded to bf16 for the P.V MFMA and the row sum
+ * FMA before exp2; t2i text rows pre-scale q instead); P is rounded to bf16 for the P.V MFMA and the row sum
  * adds the same rounded values. The running max
  * is moved lazily (only when a row's tile max exceeds it by 2^8), which
  * keeps O and l consistent while skipping the rescale on most tiles.
@@ -161,12 +161,27 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
     }
     const uint32_t ntiles = (lmax + AKT - 1) / AKT;
 
+    /* t2i text rows follow the reference's text-row kernel
+     * (h3_shaders.metal:4397-4401): q is multiplied by the softmax scale
+     * and re-rounded to bf16 before QK, and the scores are not scaled
+     * again (their exp2 factor is log2 e alone). Prefix tables (ti2i) and
+     * image rows keep bf16 q with the scale folded into the exp2 FMA. */
+    const bool prescale = !a.kv_limit && r < a.text_rows;
+    const float c = prescale ? 1.4426950408889634f : a.scale_log2;
+
     /* ---- Q^T fragments (B operand), resident for the whole loop --------- */
     bf16x8 qf[8];
     {
         const u16 *qrow = qb + (size_t)min(r, a.q_rows - 1) * a.ldq;
 #pragma unroll
         for (int s = 0; s < 8; s++) qf[s] = *(const bf16x8 *)(qrow + 16 * s + 8 * h);
+        if (prescale) { /* t2i text rows: q' = bf16(q * scale) */
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    qf[s][e] = (__bf16)((float)qf[s][e] * a.scale);
+        }
     }
     floatx16 o[4];
 #pragma unroll
@@ -251,7 +266,6 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
     };
 
     float m_run = -INFINITY, l_run = 0.0f;
-    const float c = a.scale_log2;
     /* Online-softmax step of a tile whose S is in `sc`, with the QK MFMAs of
      * the next tile (into `sn`) laid out between its VALU work. The running
      * max moves lazily: only when a row's tile max exceeds it by more than

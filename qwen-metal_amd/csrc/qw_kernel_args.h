@@ -178,6 +178,7 @@ typedef struct {
     uint32_t ldq, ldk, ldv, ldo; /* row strides in elements */
     uint32_t text_rows;          /* closed-form limits when kv_limit == NULL */
     int32_t text_causal;
+    float scale;      /* softmax scale */
     float scale_log2; /* softmax scale * log2(e) */
 } qw_attn_args;
 

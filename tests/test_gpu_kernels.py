@@ -420,7 +420,8 @@ def _attn_case(gpu, qd, oracle, rows, heads, limits_mode, batch=1, text=0, causa
     ref = np.concatenate([oracle.attention(q[b * rows:(b + 1) * rows].copy(),
                                            k[b * rows:(b + 1) * rows].copy(),
                                            v[b * rows:(b + 1) * rows].copy(), lim, rows, rows,
-                                           heads) for b in range(batch)])
+                                           heads, prescale_rows=text if limits_mode == "t2i"
+                                           else 0) for b in range(batch)])
     f = oracle.bf16_to_f32
     return rel_l2(f(got), f(ref)), cosine(f(got), f(ref))
 
@@ -440,6 +441,38 @@ def test_attention_t2i(gpu, qd, oracle, rows, heads, text, causal, batch):
     assert rel < 5e-3 and cos > 0.9999
 
 
+@pytest.mark.parametrize("causal", [1, 0])
+def test_attention_text_rows_prescale_q(gpu, qd, oracle, causal):
+    """t2i text rows contract bf16(q * scale) with K (h3_shaders.metal:
+    4397-4401). Sharp scores (|q|, |k| up to 8) make the re-rounding visible:
+    the kernel must sit much closer to the oracle with the rule than to the
+    oracle without it. The oracle rounds P to bf16 here, as the kernel's P
+    operand is, so the comparison isolates the q rule."""
+    rows, heads, text = 160, 2, 96
+    hd = heads * 128
+    rng = np.random.default_rng(41)
+    q, k, v = (bf(oracle, a * rng.uniform(-1, 1, (rows, hd))) for a in (8.0, 8.0, 1.0))
+    out = gpu.new(rows * hd, qd.BF16)
+    gpu.attention(out, gpu.put(q), gpu.put(k), gpu.put(v), 1, rows, rows, heads, hd, hd, hd, hd,
+                  text_rows=text, text_causal=causal)
+    gpu.submit()
+    f = oracle.bf16_to_f32
+    got = f(out.read().reshape(rows, hd))
+    lim = oracle.t2i_limits(rows, text, causal)
+    oracle.set_attention_p_mode(1)
+    try:
+        with_rule = f(oracle.attention(q, k, v, lim, rows, rows, heads, prescale_rows=text))
+        without = f(oracle.attention(q, k, v, lim, rows, rows, heads))
+    finally:
+        oracle.set_attention_p_mode(0)
+    e_rule = rel_l2(got[:text], with_rule[:text])
+    e_plain = rel_l2(got[:text], without[:text])
+    assert e_rule < 2.5e-3 and e_plain > 2 * e_rule, (e_rule, e_plain)
+    # image rows keep the scale in the softmax: identical in both oracles
+    assert rel_l2(got[text:], with_rule[text:]) < 5e-3
+    assert np.array_equal(with_rule[text:], without[text:])
+
+
 def test_attention_strided_qkv(gpu, qd, oracle):
     """q|k|v read from one fused [rows, 3H] buffer, as the block does."""
     rows, heads = 130, 2
@@ -456,7 +489,7 @@ def test_attention_strided_qkv(gpu, qd, oracle):
     for b in range(2):
         blk = m[b * rows:(b + 1) * rows]
         ref = oracle.attention(blk[:, :H].copy(), blk[:, H:2 * H].copy(),
-                               blk[:, 2 * H:].copy(), lim, rows, rows, heads)
+                               blk[:, 2 * H:].copy(), lim, rows, rows, heads, prescale_rows=10)
         assert rel_l2(oracle.bf16_to_f32(got[b * rows:(b + 1) * rows]),
                       oracle.bf16_to_f32(ref)) < 5e-3
 
