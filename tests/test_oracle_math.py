@@ -241,8 +241,11 @@ def test_prefix_limits_layouts(oracle, qd):
 
 def test_ti2i_reduces_to_causal_t2i(oracle):
     """The ti2i full pass over [text T; target image I] is the t2i forward
-    with causal text rows: same rows, row map (text at t = 0) and limits, so
-    the two oracle paths agree bit for bit."""
+    with causal text rows: same rows, row map (text at t = 0) and limits. The
+    one difference is the t2i text-row rule (q pre-scaled and re-rounded to
+    bf16, h3_shaders.metal:4397-4401), which the ti2i prefix kernel does not
+    apply: the two agree to the bf16 band (bit for bit with q = k = 0, see
+    test_oracle_composition.py)."""
     cfg = dict(hidden=256, heads=2, mlp_width=512, text_dim=256, z_dim=64, layers=2,
                mlp_act=0, adaln_shift=0, has_bias=0, text_causal=1, int8_weights=0)
     T, gh, gw = 6, 4, 4
@@ -254,4 +257,6 @@ def test_ti2i_reduces_to_causal_t2i(oracle):
     a = m.forward(text, T, lat, I, 0.7, cos, sin, 2)
     b = m.forward_ti2i(text, T, lat, I, [(T, 0, 0), (I, 1, 0)], 0.7, cos, sin, 2)
     m.close()
-    assert np.array_equal(a, b)
+    f = oracle.bf16_to_f32
+    assert not np.array_equal(a, b)
+    assert rel_l2(f(a), f(b)) < 1e-2
