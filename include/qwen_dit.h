@@ -245,6 +245,18 @@ int qw_dit_forward_batch_features(qw_dit *dit, const h3_gpu_tensor *text_in,
  * conditioning and final. Returns the number of stages written. */
 int qw_dit_block_profile(const qw_dit *dit, double *ms, int max_stages);
 
+/* Diagnostic trace of the t2i forward (qw_dit_forward*), for per-block
+ * parity checks; no reference counterpart (the reference dumps stages
+ * through its QWEN_* diagnostic switches instead). While set, each
+ * forward copies, on its stream: the joint hidden state after the embed
+ * into rows [0, M) of `hidden` and after block l into rows
+ * [(l + 1) M, (l + 2) M) (M = batch * rows, [M, hidden] bf16 each, so
+ * `hidden` holds (layers + 1) M hidden); and the slot-ordered modulation
+ * [2, slots * hidden] into `modulation` (may be NULL). A forward whose
+ * trace tensors are too small fails with an error. NULL, NULL stops
+ * tracing. The caller keeps ownership of both tensors. */
+int qw_dit_set_trace(qw_dit *dit, h3_gpu_tensor *hidden, h3_gpu_tensor *modulation);
+
 #ifdef __cplusplus
 }
 #endif

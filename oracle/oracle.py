@@ -129,6 +129,8 @@ def lib():
         L.qo_block.argtypes = [C.POINTER(QoModel), C.c_int, u16p, u16p, f32p,
                                f32p, u32p, C.c_uint32, C.c_uint32,
                                C.c_void_p, C.c_void_p]
+        L.qo_block_rows.argtypes = [C.POINTER(QoModel), C.c_int, u16p, u16p, f32p, f32p,
+                                    u32p, C.c_uint32, C.c_uint32, u32p, C.c_uint32, u16p]
         L.qo_final.argtypes = [C.POINTER(QoModel), u16p, u16p, u32p,
                                C.c_uint32, u16p]
         L.qo_forward.restype = C.c_int
@@ -289,6 +291,17 @@ class Model:
                                    np.ascontiguousarray(rope_sin), layers, out)
         if not ok:
             raise RuntimeError("qo_forward_ti2i failed")
+        return out
+
+    def block_rows(self, layer, hidden, modulation, rope_cos, rope_sin, row_map, rows,
+                   text_rows, sample):
+        """qo_block's output for the listed rows only: [len(sample), H]"""
+        sample = np.ascontiguousarray(sample, np.uint32)
+        out = np.empty((len(sample), self.cfg.hidden), np.uint16)
+        lib().qo_block_rows(C.byref(self.m), layer, np.ascontiguousarray(hidden),
+                            np.ascontiguousarray(modulation), np.ascontiguousarray(rope_cos),
+                            np.ascontiguousarray(rope_sin), np.ascontiguousarray(row_map),
+                            rows, text_rows, sample, len(sample), out)
         return out
 
     def block(self, layer, hidden, modulation, rope_cos, rope_sin, row_map,

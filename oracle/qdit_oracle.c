@@ -11,6 +11,7 @@
 #include <stdlib.h>
 #include <string.h>
 #ifdef _OPENMP
+#include <immintrin.h>
 #include <omp.h>
 #endif
 
@@ -287,14 +288,19 @@ static void gemm_chunk(const float *a, size_t lda, const float *b, size_t ldb,
             v8f c20 = {0}, c21 = {0}, c22 = {0}, c23 = {0};
             for (size_t kk = 0; kk < k8; kk += 8) {
                 v8f x0 = ld8(a0 + kk), x1 = ld8(a1 + kk), x2 = ld8(a2 + kk);
+                /* fused multiply-adds: the contraction's fp32 summation
+                 * order is free (any order is an fp32-accumulating linear);
+                 * only the elementwise code keeps -ffp-contract=off */
+#define QO_FMA(c, x, w) c = (v8f)_mm256_fmadd_ps((__m256)(x), (__m256)(w), (__m256)(c))
                 v8f w = ld8(b0 + kk);
-                c00 += x0 * w; c10 += x1 * w; c20 += x2 * w;
+                QO_FMA(c00, x0, w); QO_FMA(c10, x1, w); QO_FMA(c20, x2, w);
                 w = ld8(b1 + kk);
-                c01 += x0 * w; c11 += x1 * w; c21 += x2 * w;
+                QO_FMA(c01, x0, w); QO_FMA(c11, x1, w); QO_FMA(c21, x2, w);
                 w = ld8(b2 + kk);
-                c02 += x0 * w; c12 += x1 * w; c22 += x2 * w;
+                QO_FMA(c02, x0, w); QO_FMA(c12, x1, w); QO_FMA(c22, x2, w);
                 w = ld8(b3 + kk);
-                c03 += x0 * w; c13 += x1 * w; c23 += x2 * w;
+                QO_FMA(c03, x0, w); QO_FMA(c13, x1, w); QO_FMA(c23, x2, w);
+#undef QO_FMA
             }
             float r[3][4] = {
                 {hsum8(c00), hsum8(c01), hsum8(c02), hsum8(c03)},
@@ -959,6 +965,87 @@ void qo_block(const qo_model *m, int layer, uint16_t *hidden,
     if (act != wide) free(act);
     free(wide);
     free(lim);
+}
+
+void qo_block_rows(const qo_model *m, int layer, const uint16_t *hidden,
+                   const uint16_t *modulation, const float *rope_cos,
+                   const float *rope_sin, const uint32_t *row_map,
+                   uint32_t rows, uint32_t text_rows, const uint32_t *sample,
+                   uint32_t n_sample, uint16_t *out) {
+    /* qo_block restricted to the output rows listed in `sample`: every row
+     * goes through LN1 + QKV + q/k norm + RoPE (the sampled rows attend
+     * all of their keys), the rest of the block runs on the sampled rows
+     * only. Row-wise stages are identical to qo_block's; t2i limits. */
+    const qo_layer *L = &m->layer[layer];
+    size_t H = m->cfg.hidden, F = m->cfg.mlp_width, heads = m->cfg.heads;
+    uint32_t slots = m->cfg.adaln_shift ? 6 : 4;
+    int sh = m->cfg.adaln_shift;
+    size_t f1 = m->cfg.mlp_act == QO_MLP_SWIGLU ? 2 * F : F;
+    uint16_t *mod = malloc(sizeof(uint16_t) * rows * H);
+    uint16_t *qkv = malloc(sizeof(uint16_t) * rows * 3 * H);
+    uint16_t *q_s = malloc(sizeof(uint16_t) * n_sample * H);
+    uint16_t *h_s = malloc(sizeof(uint16_t) * n_sample * H);
+    uint16_t *attn = malloc(sizeof(uint16_t) * n_sample * H);
+    uint16_t *branch = malloc(sizeof(uint16_t) * n_sample * H);
+    uint16_t *mod_s = malloc(sizeof(uint16_t) * n_sample * H);
+    uint16_t *wide = malloc(sizeof(uint16_t) * n_sample * f1);
+    uint16_t *act = m->cfg.mlp_act == QO_MLP_SWIGLU
+                        ? malloc(sizeof(uint16_t) * n_sample * F)
+                        : wide;
+    uint32_t *lim_all = malloc(sizeof(uint32_t) * rows);
+    uint32_t *lim = malloc(sizeof(uint32_t) * n_sample);
+    uint32_t *rm_s = malloc(sizeof(uint32_t) * n_sample);
+    qo_t2i_limits(lim_all, rows, text_rows, m->cfg.text_causal);
+    qo_layer_norm_mod(mod, hidden, modulation, row_map, rows, H, slots, 0,
+                      sh ? 4 : -1, 1e-6f);
+    qo_apply_linear(&L->qkv, qkv, 3 * H, mod, H, rows);
+    qo_head_rms_norm(qkv, 3 * H, L->norm_q, rows, heads, 128, 1e-6f);
+    qo_head_rms_norm(qkv + H, 3 * H, L->norm_k, rows, heads, 128, 1e-6f);
+    qo_qk_rope(qkv, 3 * H, rope_cos, rope_sin, rows, heads, 128);
+    qo_qk_rope(qkv + H, 3 * H, rope_cos, rope_sin, rows, heads, 128);
+    /* sampled rows, text rows first so the t2i text rule covers a prefix */
+    uint32_t n_text = 0;
+    for (uint32_t i = 0; i < n_sample; i++) n_text += sample[i] < text_rows;
+    uint32_t *order = malloc(sizeof(uint32_t) * n_sample);
+    uint32_t no = 0;
+    for (int pass = 0; pass < 2; pass++)
+        for (uint32_t i = 0; i < n_sample; i++)
+            if ((sample[i] < text_rows) == (pass == 0)) order[no++] = i;
+    for (uint32_t j = 0; j < n_sample; j++) {
+        const uint32_t r = sample[order[j]];
+        memcpy(q_s + (size_t)j * H, qkv + (size_t)r * 3 * H, sizeof(uint16_t) * H);
+        memcpy(h_s + (size_t)j * H, hidden + (size_t)r * H, sizeof(uint16_t) * H);
+        lim[j] = lim_all[r];
+        rm_s[j] = row_map[r];
+    }
+    qo_attention_ex(attn, H, q_s, H, qkv + H, 3 * H, qkv + 2 * H, 3 * H, lim,
+                    n_sample, rows, heads, 128, 1.0f / sqrtf(128.0f), n_text);
+    qo_apply_linear(&L->out, branch, H, attn, H, n_sample);
+    qo_gate(h_s, h_s, branch, modulation, rm_s, n_sample, H, slots, 2);
+    qo_layer_norm_mod(mod_s, h_s, modulation, rm_s, n_sample, H, slots, 1,
+                      sh ? 5 : -1, 1e-6f);
+    qo_apply_linear(&L->fc1, wide, f1, mod_s, H, n_sample);
+    if (m->cfg.mlp_act == QO_MLP_SWIGLU)
+        qo_swiglu(act, wide, n_sample, F);
+    else
+        qo_gelu_tanh(act, wide, (size_t)n_sample * F);
+    qo_apply_linear(&L->fc2, branch, H, act, F, n_sample);
+    qo_gate(h_s, h_s, branch, modulation, rm_s, n_sample, H, slots, 3);
+    for (uint32_t j = 0; j < n_sample; j++)
+        memcpy(out + (size_t)order[j] * H, h_s + (size_t)j * H, sizeof(uint16_t) * H);
+    free(order);
+    free(mod);
+    free(qkv);
+    free(q_s);
+    free(h_s);
+    free(attn);
+    free(branch);
+    free(mod_s);
+    if (act != wide) free(act);
+    free(wide);
+    free(lim_all);
+    free(lim);
+    free(rm_s);
 }
 
 void qo_final(const qo_model *m, const uint16_t *hidden,

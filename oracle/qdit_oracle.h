@@ -236,6 +236,14 @@ void qo_block(const qo_model *m, int layer, uint16_t *hidden,
               const float *rope_sin, const uint32_t *row_map, uint32_t rows,
               uint32_t text_rows, const uint32_t *limits,
               uint16_t *debug_attn);
+/* qo_block evaluated for the output rows listed in sample[n_sample] only
+ * (all rows still feed K and V): out [n_sample, H] in sample order. t2i
+ * limits; the same arithmetic as qo_block for those rows. */
+void qo_block_rows(const qo_model *m, int layer, const uint16_t *hidden,
+                   const uint16_t *modulation, const float *rope_cos,
+                   const float *rope_sin, const uint32_t *row_map,
+                   uint32_t rows, uint32_t text_rows, const uint32_t *sample,
+                   uint32_t n_sample, uint16_t *out);
 /* qwen_dit.m:1478-1496 */
 void qo_final(const qo_model *m, const uint16_t *hidden,
               const uint16_t *norm_out_mod, const uint32_t *row_map,

@@ -62,6 +62,8 @@ struct qw_dit {
     uint32_t rm_rows, rm_text, rm_batch;
     int profile;
     double prof_ms[P_COUNT];
+    /* qw_dit_set_trace: per-block hidden states and the modulation */
+    h3_gpu_tensor *trace_hidden, *trace_mod;
     /* LoRA adapters, in stack order; while any is active, base[4 l + j]
      * keeps layer l's base weight j (qkv, out, fc1, fc2) and the layer
      * holds the fused copy */
@@ -1236,10 +1238,25 @@ static int forward_impl(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_r
         return error && *error ? 0 : set_error(error, error_size, "conditioning failed");
     prof_end(d, P_COND);
 
-    for (uint32_t l = 0; l < d->cfg.layers; l++)
+    const size_t MH = (size_t)M * H;
+    if (d->trace_hidden) {
+        if (h3_gpu_tensor_elements(d->trace_hidden) < (size_t)(d->cfg.layers + 1) * MH ||
+            (d->trace_mod && h3_gpu_tensor_elements(d->trace_mod) < (size_t)2 * S * H))
+            return set_error(error, error_size, "trace tensors too small for %u layers of %u rows",
+                             d->cfg.layers, M);
+        if (!h3_gpu_copy_bf16(g, d->trace_hidden, 0, d->joint, 0, MH) ||
+            (d->trace_mod &&
+             !h3_gpu_copy_bf16(g, d->trace_mod, 0, d->modulation, 0, (size_t)2 * S * H)))
+            return set_error(error, error_size, "trace copy failed: %s", h3_gpu_error(g));
+    }
+    for (uint32_t l = 0; l < d->cfg.layers; l++) {
         if (!block_run(d, (int)l, d->joint, batch, rows, text_rows, d->modulation, rope_cos,
                        rope_sin, d->row_map, NULL, NULL, NULL, NULL, NULL))
             return set_error(error, error_size, "block %u kernel failed: %s", l, h3_gpu_error(g));
+        if (d->trace_hidden &&
+            !h3_gpu_copy_bf16(g, d->trace_hidden, (size_t)(l + 1) * MH, d->joint, 0, MH))
+            return set_error(error, error_size, "trace copy failed: %s", h3_gpu_error(g));
+    }
 
     prof_begin(d);
     const int sh = d->cfg.adaln_shift;
@@ -1247,8 +1264,18 @@ static int forward_impl(qw_dit *d, const h3_gpu_tensor *text_in, uint32_t text_r
                                               M, H, sh ? 2 : 1, 0, sh ? 1 : -1, 1e-6f) &&
              plain(d, &d->proj_out, output, d->ws_mod, M, QW_LINEAR_STORE);
     prof_end(d, P_FINAL);
-    (void)S;
     if (!ok) return set_error(error, error_size, "final projection failed: %s", h3_gpu_error(g));
+    return 1;
+}
+
+int qw_dit_set_trace(qw_dit *d, h3_gpu_tensor *hidden, h3_gpu_tensor *modulation) {
+    if (!d) return 0;
+    if (!hidden && modulation) return 0;
+    if ((hidden && h3_gpu_tensor_dtype(hidden) != H3_GPU_BF16) ||
+        (modulation && h3_gpu_tensor_dtype(modulation) != H3_GPU_BF16))
+        return 0;
+    d->trace_hidden = hidden;
+    d->trace_mod = modulation;
     return 1;
 }
 

@@ -162,6 +162,7 @@ SIGNATURES = {
     "qw_dit_forward_batch_features": (C.c_int, [vp, vp, u32, vp, u32, u32, vp, sz, vp, vp, vp,
                                                 C.c_char_p, sz]),
     "qw_dit_block_profile": (C.c_int, [vp, vp, C.c_int]),
+    "qw_dit_set_trace": (C.c_int, [vp, vp, vp]),
     "qw_dit_apply_lora": (C.c_int, [vp, C.c_char_p, C.c_float, C.c_char_p, sz]),
     "qw_dit_remove_lora": (C.c_int, [vp, C.c_char_p, C.c_char_p, sz]),
     "qw_dit_switch_lora": (C.c_int, [vp, C.c_char_p, C.c_float, C.c_char_p, sz]),

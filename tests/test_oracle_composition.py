@@ -555,3 +555,25 @@ def test_uniform_attention_forward_matches_numpy_chain(oracle):
     ok, err = close(f, want, rel=2 ** -4, abs_=2 ** -5)
     assert ok, err
     m.close()
+
+
+@VARIANTS
+def test_block_rows_equals_block(oracle, variant):
+    """qo_block_rows (the sampled-row form used at full size) gives exactly
+    qo_block's rows, text and image rows interleaved in any order."""
+    o = oracle
+    m, cfg = model(o, variant)
+    H = cfg["hidden"]
+    rng = np.random.default_rng(12)
+    T, gh, gw = 9, 3, 5
+    rows = T + gh * gw
+    hid = o.f32_to_bf16(rng.standard_normal((rows, H)))
+    mod = slot_values(o, cfg, rng)
+    cos, sin = o.rope_tables(T, gh, gw)
+    rm = (np.arange(rows) < T).astype(np.uint32)
+    full = hid.copy()
+    m.block(1, full, mod, cos, sin, rm, rows, T)
+    sample = np.array([rows - 1, 0, 12, 3, T, 8, 17], np.uint32)
+    got = m.block_rows(1, hid, mod, cos, sin, rm, rows, T, sample)
+    assert np.array_equal(got, full.reshape(rows, H)[sample])
+    m.close()
