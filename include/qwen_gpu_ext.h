@@ -124,6 +124,18 @@ typedef struct {
     float eps;
 } qw_linear_desc;
 int qw_gpu_linear(h3_gpu *gpu, const qw_linear_desc *desc);
+/* No counterpart in the reference. For callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): qw_gpu_linear with every workspace in
+ * one static per-GPU device buffer of 32 MiB + 4 KiB, held until the
+ * process ends. It calls no hipMalloc / hipFree. int8 weights are widened
+ * inside the GEMM loop (no bf16 staging copy); split tiles are used only as
+ * far as their fp32 partials fit the buffer (at most 128 pieces), so long-K
+ * linears may split less than qw_gpu_linear does (same bar: within one
+ * bf16 ulp of it, or of its cancellation bound). A split that would need
+ * more fails with an error. Calls on one GPU share that buffer: calls that
+ * overlap on one GPU (several streams or threads at once) race. */
+int qw_gpu_linear_static(h3_gpu *gpu, const qw_linear_desc *desc);
 
 /* Fused per-head RMSNorm (single rounding, h3_shaders.metal:4309-4329) and
  * interleaved RoPE (h3_shaders.metal:4864-4896) over q and k in one

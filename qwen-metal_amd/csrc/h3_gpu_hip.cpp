@@ -20,6 +20,7 @@
 #include <algorithm>
 
 #include "qw_kernel_args.h"
+#include "qw_static_scratch.h"
 
 enum {
     K_LN_MOD, K_RMS_ONE, K_QK_NORM_ROPE, K_GATE, K_ACT, K_SWIGLU, K_CAST,
@@ -27,7 +28,7 @@ enum {
     /* GEMM kernels in QW_LINEAR_* epilogue order (store, gelu, gate, qknorm) */
     K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_GEMM_I8_QKN_W8,
     K_GEMM_BF16_STORE_D, K_GEMM_BF16_GELU_D, K_GEMM_BF16_GATE_D, K_GEMM_BF16_QKN_D, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
-    K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_COUNT
+    K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_ZERO, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_bf16", "qw_rms_norm_one_bf16", "qw_qk_norm_rope_bf16",
@@ -38,7 +39,8 @@ static const char *k_names[K_COUNT] = {
     "qw_gemm_bf16_store_d", "qw_gemm_bf16_gelu_d", "qw_gemm_bf16_gate_d", "qw_gemm_bf16_qkn_d",
     "qw_widen_i8_bf16",
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16",
-    "qw_gemv_bf16_store", "qw_gemv_bf16_gelu", "qw_gemv_i8_store", "qw_gemv_i8_gelu"};
+    "qw_gemv_bf16_store", "qw_gemv_bf16_gelu", "qw_gemv_i8_store", "qw_gemv_i8_gelu",
+    "qw_zero_u32"};
 
 struct h3_gpu {
     int device;
@@ -59,6 +61,9 @@ struct h3_gpu {
     uint32_t cus;      /* compute units */
     float *sk_part;    /* split-tile partials: 256 x 256 fp32 each */
     uint32_t *sk_flag; /* split-tile piece counters, 0 between launches */
+    /* this device's copy of the static workspace (qw_static_scratch.hip):
+     * partials, then QW_STATIC_FLAGS counters */
+    unsigned char *static_scratch;
 };
 
 struct h3_gpu_tensor {
@@ -153,6 +158,7 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     g->cus = 0;
     g->sk_part = NULL;
     g->sk_flag = NULL;
+    g->static_scratch = NULL;
     hipError_t e = hipModuleLoad(&g->module, path.c_str());
     if (e != hipSuccess) {
         set_err(error, error_size, "hipModuleLoad(%s): %s", path.c_str(), hipGetErrorString(e));
@@ -188,6 +194,19 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
         return NULL;
     }
     g->cus = (uint32_t)cus;
+    {
+        /* once per device, with the device current: the address of its
+         * copy of the no-allocation entry points' static workspace */
+        void *ss = NULL;
+        char se[256] = {0};
+        if (qw_static_scratch_address(device, &ss, se, sizeof(se)) != 0) {
+            set_err(error, error_size, "%s", se);
+            hipModuleUnload(g->module);
+            delete g;
+            return NULL;
+        }
+        g->static_scratch = (unsigned char *)ss;
+    }
     if (hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking) != hipSuccess ||
         hipEventCreate(&g->timer0) != hipSuccess || hipEventCreate(&g->timer1) != hipSuccess ||
         hipEventCreate(&g->chain0) != hipSuccess || hipEventCreate(&g->chain1) != hipSuccess) {
@@ -805,14 +824,17 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
  * measured slower when split, K = 12288 ones faster), and
  * R s <= QW_SPLIT_MAX_PIECES * cus bounds the partial workspace. */
 #define QW_SPLIT_MAX_PIECES 2
-static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps) {
+static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps,
+                             uint64_t max_pieces = (uint64_t)QW_SPLIT_MAX_PIECES * 1024u) {
     const uint32_t min_steps = 32;
     const uint32_t G = g->cus, R = tiles % G;
     if (R == 0) return 1;
     uint32_t best = 1;
     double best_t = 0.9;
     for (uint32_t s = 2; s <= 8; s++) {
-        if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * G || ksteps < min_steps * s) break;
+        if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * G || (uint64_t)R * s > max_pieces ||
+            ksteps < min_steps * s)
+            break;
         const double t = (double)((R * s + G - 1) / G) / s + 0.02 * (s - 1);
         if (t < best_t) {
             best_t = t;
@@ -822,7 +844,10 @@ static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps) {
     return best;
 }
 
-extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
+/* no_alloc: the workspace-free form behind qw_gpu_linear_static (int8
+ * weights widen inside the GEMM loop; split-tile partials and counters live
+ * in the static workspace, as far as it holds them) */
+static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     if (!g || !d) return 0;
     REQ_DT(d->out, H3_GPU_BF16, "linear out");
     REQ_DT(d->in, H3_GPU_BF16, "linear in");
@@ -907,7 +932,7 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
      * unscaled) and run the bf16 GEMM, whose epilogue applies the per-row
      * scale to the fp32 sums -- the same arithmetic as the int8 kernels,
      * without their in-loop widening. */
-    const int widen = int8 && d->rows >= QW_WIDEN_MIN_ROWS;
+    const int widen = int8 && !no_alloc && d->rows >= QW_WIDEN_MIN_ROWS;
     const void *wptr = d->weight->ptr;
     if (widen) {
         const size_t n = (size_t)d->cols * d->k, bytes = n * 2;
@@ -919,6 +944,7 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
             if (hipMalloc(&g->widen, bytes) != hipSuccess)
                 return fail(g, "linear: widen buffer allocation (%zu bytes) failed", bytes);
             g->widen_bytes = bytes;
+            g->stats.allocated_bytes += bytes; /* runtime workspaces count too */
         }
         if (!widen_launch(g, (uint16_t *)g->widen, (const int8_t *)d->weight->ptr, n)) return 0;
         wptr = g->widen;
@@ -965,12 +991,36 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     a.sk_part = NULL;
     a.sk_flag = NULL;
     uint32_t grid = tiles;
-    {
+    if (no_alloc) {
+        const uint32_t s = split_choice(g, tiles, d->k / 64, QW_STATIC_PARTS);
+        if (s > 1) {
+            const uint32_t R = tiles % g->cus;
+            const size_t need = (size_t)R * s * QW_STATIC_PART_BYTES;
+            if (need > (size_t)QW_STATIC_PARTS * QW_STATIC_PART_BYTES || R > QW_STATIC_FLAGS)
+                return fail(g, "linear_static: %u split pieces need %zu bytes of partials, over "
+                               "the static workspace's %u pieces", R * s, need,
+                            QW_STATIC_PARTS);
+            uint32_t *flags = (uint32_t *)(g->static_scratch +
+                                           (size_t)QW_STATIC_PARTS * QW_STATIC_PART_BYTES);
+            /* the counters must start at zero: a previous call leaves them
+             * zero, but one that did not complete might not */
+            qw_zero_args za;
+            za.p = flags;
+            za.count = R;
+            if (!launch(g, K_ZERO, dim3(blocks_for(R, 256)), dim3(256), za)) return 0;
+            a.dp_tiles = tiles - R;
+            a.split = s;
+            a.sk_part = (float *)g->static_scratch;
+            a.sk_flag = flags;
+            grid = a.dp_tiles + R * s;
+        }
+    } else {
         const uint32_t s = split_choice(g, tiles, d->k / 64);
         if (s > 1) {
             if (!g->sk_part) {
                 hipStreamSynchronize(g->stream);
                 const size_t n = (size_t)QW_SPLIT_MAX_PIECES * g->cus;
+                g->stats.allocated_bytes += n * 256 * 256 * 4 + (size_t)g->cus * 4;
                 if (hipMalloc((void **)&g->sk_part, n * 256 * 256 * 4) != hipSuccess) {
                     g->sk_part = NULL;
                     return fail(g, "linear: split-tile workspace allocation failed");
@@ -998,6 +1048,13 @@ extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) {
     if (kid >= K_GEMM_BF16_STORE_D && a.split == 1 && grid > g->cus && g->cus % 8 == 0)
         grid = g->cus;
     return launch(g, kid, dim3(grid), dim3(threads), a);
+}
+
+extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) { return linear_impl(g, d, 0); }
+
+extern "C" int qw_gpu_linear_static(h3_gpu *g, const qw_linear_desc *d) {
+    if (g && !g->static_scratch) return fail(g, "linear_static: no static workspace");
+    return linear_impl(g, d, 1);
 }
 
 static qw_linear_desc plain_linear(h3_gpu_tensor *out, const h3_gpu_tensor *in,
@@ -1043,6 +1100,7 @@ static void *scratch(h3_gpu *g, size_t bytes) {
     g->scratch_bytes = 0;
     if (hipMalloc(&g->scratch, bytes) != hipSuccess) return NULL;
     g->scratch_bytes = bytes;
+    g->stats.allocated_bytes += bytes;
     return g->scratch;
 }
 

@@ -356,3 +356,10 @@ QW_KERNEL void __launch_bounds__(256) qw_copy2d(qw_copy2d_args a) {
     ((uint32_t *)((char *)a.dst + r * a.dst_stride))[c] =
         ((const uint32_t *)((const char *)a.src + r * a.src_stride))[c];
 }
+
+/* n u32 words set to zero (counters that must start at zero; a kernel, not
+ * hipMemsetAsync, so the clear can sit inside a captured graph) */
+QW_KERNEL void __launch_bounds__(256) qw_zero_u32(qw_zero_args a) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < a.count) a.p[i] = 0u;
+}

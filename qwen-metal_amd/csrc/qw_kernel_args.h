@@ -160,6 +160,11 @@ typedef struct {
     uint64_t rows, row_bytes, dst_stride, src_stride; /* bytes */
 } qw_copy2d_args;
 
+typedef struct {
+    uint32_t *p;
+    uint64_t count;
+} qw_zero_args;
+
 /* Waves per attention workgroup (32 queries each). The host reads the
  * workgroup size back from the code object. */
 #ifndef QW_ATTN_WAVES

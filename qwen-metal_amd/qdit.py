@@ -131,6 +131,7 @@ SIGNATURES = {
     "qw_gpu_layer_norm_mod_shift_bf16": (C.c_int, [vp, vp, vp, vp, vp, u32, u32, u32, u32,
                                                    C.c_int32, C.c_float]),
     "qw_gpu_linear": (C.c_int, [vp, C.POINTER(LinearDesc)]),
+    "qw_gpu_linear_static": (C.c_int, [vp, C.POINTER(LinearDesc)]),
     "qw_gpu_qk_norm_rope_bf16": (C.c_int, [vp, vp, u32, u32, u32, u32, vp, vp, vp, vp, u32,
                                            C.c_float]),
     "qw_gpu_attention_bf16": (C.c_int, [vp, C.POINTER(AttentionDesc)]),
@@ -337,15 +338,17 @@ class Gpu:
     # ---- dispatch helpers (enqueue only) ----
     def linear(self, out, inp, weight, rows, k, cols, bias=None, wscale=None,
                epilogue=LINEAR_STORE, ldc=None, lda=None, out_offset=0, in_offset=0,
-               modulation=None, row_map=None, slots=0, gate_slot=0, qknorm=None):
+               modulation=None, row_map=None, slots=0, gate_slot=0, qknorm=None,
+               no_alloc=False):
         """qknorm = (norm_q, norm_k, rope_cos, rope_sin, rope_rows, eps) with
-        epilogue LINEAR_QKNORM"""
+        epilogue LINEAR_QKNORM; no_alloc: qw_gpu_linear_static"""
         nq, nk, rc, rs, rr, eps = qknorm if qknorm else (None, None, None, None, 0, 0.0)
         h = lambda t: t.h if t is not None else None  # noqa: E731
         d = LinearDesc(out.h, out_offset, ldc or cols, inp.h, in_offset, lda or k, weight.h,
                        h(wscale), h(bias), rows, k, cols, epilogue, h(modulation), h(row_map),
                        slots, gate_slot, h(nq), h(nk), h(rc), h(rs), rr, eps)
-        self.check(lib().qw_gpu_linear(self.h, C.byref(d)), "linear")
+        fn = lib().qw_gpu_linear_static if no_alloc else lib().qw_gpu_linear
+        self.check(fn(self.h, C.byref(d)), "linear")
 
     def attention(self, out, q, k, v, batch, q_rows, kv_rows, heads, ldq, ldk, ldv, ldo,
                   q_offset=0, k_offset=0, v_offset=0, kv_limit=None, text_rows=0,

@@ -1,0 +1,81 @@
+"""qw_gpu_linear_static (the entry point that allocates nothing) against
+qw_gpu_linear on the same inputs, through the C-ABI: two calls in a row,
+the second on a smaller input, each within one bf16 ulp of the allocating
+entry point (or within 2^-14 sum |x||w| where the sum cancels), and no
+device allocation by the runtime across the static calls."""
+import numpy as np
+import pytest
+
+from conftest import ulp_diff
+
+pytestmark = pytest.mark.gpu
+SEED = 77
+
+
+def _close(oracle, got, ref, mag, epi):
+    """the linear bar of the parity tests: one ulp (or 2^-14 sum |x||w|);
+    after GELU or the residual gate one flip of the linear's rounding plus
+    one output rounding: two ulps (or 2^-13 sum |x||w|)"""
+    ulps, frac = (1, 2.0 ** -14) if epi == "store" else (2, 2.0 ** -13)
+    d = ulp_diff(got, ref)
+    diff = np.abs(oracle.bf16_to_f32(got).astype(np.float64) - oracle.bf16_to_f32(ref))
+    ok = (d <= ulps) | (diff <= frac * mag)
+    assert ok.all(), (int(d.max()), np.flatnonzero(~ok)[:5])
+
+
+# (k, n, int8, epilogue, rows of the first call, rows of the second)
+CASES = [
+    # K = 12288: split tiles in both entry points (static: fewer pieces)
+    (12288, 3072, False, "store", 1152, 600),
+    # int8: qw_gpu_linear widens to bf16 first (>= 512 rows), the static
+    # form widens inside the GEMM loop
+    (3072, 1536, True, "gelu", 1100, 520),
+    (3072, 3072, True, "gate", 700, 64),
+]
+
+
+@pytest.mark.parametrize("k,n,int8,epi,m1,m2", CASES)
+def test_linear_static_matches_linear(qd, oracle, k, n, int8, epi, m1, m2):
+    gpu = qd.Gpu()  # a fresh context: its runtime owns no workspace yet
+    try:
+        E = {"store": qd.LINEAR_STORE, "gelu": qd.LINEAR_GELU, "gate": qd.LINEAR_GATE}[epi]
+        x = oracle.fill_normal_bf16(m1 * k, SEED, 1)
+        w = oracle.fill_normal_bf16(n * k, SEED, 2, 0.02)
+        b = oracle.fill_normal_bf16(n, SEED, 3, 0.02)
+        if int8:
+            q, s = oracle.quantize_int8_rows(w, n, k)
+            wt, st = gpu.put(q), gpu.put(s)
+        else:
+            wt, st = gpu.put(w), None
+        xt, bt = gpu.put(x), gpu.put(b)
+        res = oracle.fill_normal_bf16(m1 * n, SEED, 4)
+        gmod = oracle.fill_normal_bf16(2 * 4 * n, SEED, 5, 0.3)
+        rm = (np.arange(m1) % 3 == 0).astype(np.uint32)
+        gate = dict(modulation=gpu.put(gmod), row_map=gpu.put(rm), slots=4, gate_slot=2) \
+            if epi == "gate" else {}
+        absx, absw = x & np.uint16(0x7FFF), w & np.uint16(0x7FFF)
+        outs = {}
+        for no_alloc in (False, True):
+            outs[no_alloc] = []
+            for rows in (m1, m2):
+                out = gpu.put(res[:rows * n].copy())  # the GATE epilogue adds into it
+                gpu.submit()
+                before = gpu.stats().allocated_bytes
+                gpu.linear(out, xt, wt, rows, k, n, bias=bt, wscale=st, epilogue=E,
+                           no_alloc=no_alloc, **gate)
+                gpu.submit()
+                grew = gpu.stats().allocated_bytes > before
+                if no_alloc:
+                    assert not grew
+                elif rows == m1:
+                    # the allocating entry point's first call does allocate
+                    # its workspace (split partials or the int8 widening
+                    # buffer): the check above would see an allocation
+                    assert grew
+                outs[no_alloc].append(out.read())
+        for i, rows in enumerate((m1, m2)):
+            mag = oracle.bf16_to_f32(oracle.linear(absx[:rows * k].copy(), absw, None, rows, k,
+                                                   n)).ravel()
+            _close(oracle, outs[True][i], outs[False][i], mag, epi)
+    finally:
+        gpu.close()
