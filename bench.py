@@ -11,14 +11,15 @@ inputs are seeded synthetic data generated on the device (no checkpoint).
 
 Timed region: K forward steps (embed, conditioning, 32 blocks, final head)
 with every input already resident in HBM, bracketed by a device sync and
-hipEvents on the library's stream. The dominant kernel (the up-projection
-GEMM, M=8704 K=3072 N=12288, GELU epilogue, on the int8 weight widened to
-bf16) is timed the same way, on the same stream, for the roofline entry;
+hipEvents on the library's stream. The dominant kernel (the down-projection
+GEMM, M=8704 K=12288 N=3072, residual-gate epilogue, on the int8 weight
+widened to bf16) is timed the same way, on the same stream, for the
+roofline entry;
 every other linear shape and the attention kernel are timed alongside for
 the breakdown.
 
-cpu_baseline: the CPU oracle (oracle/, OpenMP) runs ONE of the 32 blocks for
-ONE of the 2 CFG branches at the full 4352-row shape, scaled x64 to a step.
+cpu_baseline: the CPU oracle (oracle/, OpenMP) on BASELINE configs[0]-[2]
+(block, linear sweep, SDPA; 1 warm-up + median of 5), composed to a step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
        python bench.py --profile-kernel   (launches for rocprofv3 --pmc)
@@ -83,8 +84,11 @@ def kernel_breakdown(qd, gpu, reps=10):
     a = gpu.new(M * F, qd.BF16)
     out = gpu.new(M * 3 * H, qd.BF16)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, a.h, 0, M * F, 1, 1, 1.0, 0.0), "fill")
-    shapes = {"qkv": (H, 3 * H, qd.LINEAR_STORE), "out": (H, H, qd.LINEAR_STORE),
-              "up": (H, F, qd.LINEAR_GELU), "down": (F, H, qd.LINEAR_STORE)}
+    # the step's epilogues: q/k norm + RoPE, residual gate, GELU, residual gate
+    shapes = {"qkv": (H, 3 * H, qd.LINEAR_QKNORM), "out": (H, H, qd.LINEAR_GATE),
+              "up": (H, F, qd.LINEAR_GELU), "down": (F, H, qd.LINEAR_GATE)}
+    R = TEXT + GH * GW
+    ep = epilogue_operands(qd, gpu, M, R)
     res = {}
     for name, (k, n, epi) in shapes.items():
         wb = gpu.new(n * k, qd.BF16)
@@ -93,10 +97,11 @@ def kernel_breakdown(qd, gpu, reps=10):
         gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, wb.h, 0, n * k, 1, 2, 0.02, 0.0), "fill")
         gpu.check(L.h3_gpu_quantize_weight_int8(gpu.h, q.h, s.h, wb.h, n, k), "quant")
         big = gpu.new(M * n, qd.BF16) if n > 3 * H else out
-        full = lambda: gpu.linear(big, a, q, M, k, n, wscale=s, epilogue=epi)  # noqa: E731
+        kw = ep.get(epi, {})
+        full = lambda: gpu.linear(big, a, q, M, k, n, wscale=s, epilogue=epi, **kw)  # noqa
         widen = lambda: gpu.check(L.qw_gpu_widen_int8_bf16(gpu.h, wb.h, q.h, n * k),  # noqa
                                   "widen")
-        gemm = lambda: gpu.linear(big, a, wb, M, k, n, wscale=s, epilogue=epi)  # noqa: E731
+        gemm = lambda: gpu.linear(big, a, wb, M, k, n, wscale=s, epilogue=epi, **kw)  # noqa
         full()
         ms = time_ms(gpu, full, reps)
         widen()
@@ -113,7 +118,6 @@ def kernel_breakdown(qd, gpu, reps=10):
     qkv = gpu.new(M * 3 * H, qd.BF16)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, qkv.h, 0, M * 3 * H, 1, 3, 1.0, 0.0), "fill")
     att = gpu.new(M * H, qd.BF16)
-    R = TEXT + GH * GW
     run = lambda: gpu.attention(att, qkv, qkv, qkv, BATCH, R, R, CFG["heads"], 3 * H, 3 * H,  # noqa
                                 3 * H, H, 0, H, 2 * H, text_rows=TEXT, text_causal=0)
     run()
@@ -124,11 +128,60 @@ def kernel_breakdown(qd, gpu, reps=10):
     return res
 
 
+def sweep_4352(qd, gpu, reps=10):
+    """BASELINE configs[1] on the GPU: the four bf16 linears at M = 4352
+    with bias (plain store), W N(0, 0.02), X N(0, 1), HIP events on the
+    library's stream."""
+    H, F, M = CFG["hidden"], CFG["mlp_width"], TEXT + GH * GW
+    L = qd.lib()
+    x = gpu.new(M * F, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, x.h, 0, x.n, 1, 11, 1.0, 0.0), "fill")
+    out = gpu.new(M * F, qd.BF16)
+    res = {}
+    for name, k, n in (("qkv", H, 3 * H), ("out", H, H), ("up", H, F), ("down", F, H)):
+        w, b = gpu.new(n * k, qd.BF16), gpu.new(n, qd.BF16)
+        gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, w.h, 0, w.n, 1, 12, 0.02, 0.0), "fill")
+        gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, b.h, 0, b.n, 1, 13, 0.02, 0.0), "fill")
+        run = lambda: gpu.linear(out, x, w, M, k, n, bias=b)  # noqa: E731
+        run()
+        ms = time_ms(gpu, run, reps)
+        fl = 2.0 * M * n * k
+        res[name] = {"M": M, "K": k, "N": n, "ms": ms, "tflops": fl / ms / 1e9,
+                     "frac_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS}
+        w.free()
+        b.free()
+    x.free()
+    out.free()
+    return res
+
+
+def epilogue_operands(qd, gpu, M, R):
+    """Operands of the step's fused epilogues: the modulation (6 slots, gate
+    slots 2 / 3 through the row map of the batch-2 stack) and the q/k norm
+    weights with the joint RoPE tables."""
+    H = CFG["hidden"]
+    L = qd.lib()
+    mod = gpu.new(2 * 6 * H, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, mod.h, 0, mod.n, 1, 5, 0.3, 0.0), "fill")
+    rm = np.tile((np.arange(R) < TEXT).astype(np.uint32), M // R)
+    nw = gpu.new(2 * 128, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, nw.h, 0, nw.n, 1, 6, 0.02, 1.0), "fill")
+    cos = np.empty((R, 64), np.float32)
+    sin = np.empty((R, 64), np.float32)
+    L.qw_pipe_rope_tables_host(TEXT, GH, GW, cos.ctypes.data, sin.ctypes.data)
+    keep = [mod, nw, gpu.put(rm), gpu.put(cos), gpu.put(sin)]
+    nq, nk = nw.view(0, 128), nw.view(128, 128)
+    keep += [nq, nk]
+    return {qd.LINEAR_GATE: dict(modulation=mod, row_map=keep[2], slots=6, gate_slot=3),
+            qd.LINEAR_QKNORM: dict(qknorm=(nq, nk, keep[3], keep[4], R, 1e-6)),
+            "keep": keep}
+
+
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, calibrated against
     a copy kernel of known size), or None when it has not been measured."""
-    p = os.path.join(ROOT, "profiles", "gemm_up_bf16_gelu_d_traffic.md")
+    p = os.path.join(ROOT, "profiles", "gemm_down_bf16_gate_d_traffic.md")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -138,37 +191,73 @@ def measured_traffic():
     return None
 
 
-def cpu_baseline(blocks=3):
-    """`blocks` of the 32 blocks, one CFG branch, full rows, on the host
-    oracle; scaled to a step (32 blocks x 2 branches)."""
+def _median_ms(fn, runs=5):
+    fn()  # warm-up
+    ts = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t) * 1e3)
+    return float(np.median(ts)), ts
+
+
+def cpu_baseline(runs=5):
+    """The CPU oracle (oracle/, C11 + OpenMP, fp32 accumulation) on the
+    host cores, per BASELINE configs[0]-[2]: one warm-up then the median of
+    `runs` timed runs (perf_counter, i.e. CLOCK_MONOTONIC) of
+      configs[0]  one block at 64 text + 256 image rows (int8 weights off),
+      configs[1]  the four linears at M = 4352 (bf16 weights, bias),
+      configs[2]  the B2 x 24-head SDPA over 256 + 4096 rows.
+    value: a step of the workload composed from those medians: 32 layers x
+    (2 CFG branches x the four M = 4352 linears + the batch-2 SDPA), i.e.
+    everything but the bandwidth-bound elementwise work (under 5% of the
+    step's time on the CPU; it is in configs[0]'s block time)."""
     from oracle import oracle as o
-    R, H = TEXT + GH * GW, CFG["hidden"]
-    t0 = time.time()
-    m = o.Model(dict(CFG, layers=blocks), SEED, blocks)
-    hid = o.fill_normal_bf16(R * H, SEED, 990)
+    L = o.lib()
+    H, F, hd = CFG["hidden"], CFG["mlp_width"], CFG["heads"] * 128
+    res = {}
+    # configs[0]: one block, 64 + 256 rows
+    T1, R1 = 64, 64 + 256
+    m = o.Model(dict(CFG, layers=1, int8_weights=0), SEED, 1)
+    hid0 = o.fill_normal_bf16(R1 * H, SEED, 990)
     mod = o.fill_normal_bf16(2 * 6 * H, SEED, 991, 0.2)
-    rm = (np.arange(R) < TEXT).astype(np.uint32)
-    cos, sin = o.rope_tables(TEXT, GH, GW)
-    setup = time.time() - t0
-    t1 = time.time()
-    for layer in range(blocks):
-        m.block(layer, hid, mod, cos, sin, rm, R, TEXT)
-    block_s = (time.time() - t1) / blocks
+    rm = (np.arange(R1) < T1).astype(np.uint32)
+    c1, s1 = o.rope_tables(T1, 16, 16)
+    med, ts = _median_ms(lambda: m.block(0, hid0.copy(), mod, c1, s1, rm, R1, T1), runs)
     m.close()
-    per_step_ms = block_s * 1e3 * CFG["layers"] * BATCH
-    return {"value": per_step_ms, "unit": "ms/step", "cores": o.lib().qo_num_threads(),
-            "kind": "port",
-            "sample": f"{blocks} of {CFG['layers']} blocks x 1 of {BATCH} CFG branches at the "
-                      f"full {R}-row shape (int8 weights): {block_s:.2f} s per block measured, "
-                      f"scaled x{CFG['layers'] * BATCH}; weight generation {setup:.1f} s "
-                      f"excluded"}
+    res["block_320"] = {"median_ms": med, "runs_ms": ts}
+    # configs[1]: the sweep at M = 4352
+    M = TEXT + GH * GW
+    x = o.fill_normal_bf16(M * F, SEED, 992)
+    sweep = {}
+    for name, k, n in (("qkv", H, 3 * H), ("out", H, H), ("up", H, F), ("down", F, H)):
+        w = o.fill_normal_bf16(n * k, SEED, 993, 0.02)
+        b = o.fill_normal_bf16(n, SEED, 994, 0.02)
+        xs = x[:M * k]
+        med, ts = _median_ms(lambda: o.linear(xs, w, b, M, k, n), runs)
+        sweep[name] = {"median_ms": med, "gflops": 2e-6 * M * n * k / med}
+    res["sweep_4352"] = sweep
+    # configs[2]: SDPA B2 x 24 heads x 4352
+    q, k_, v = (o.fill_normal_bf16(M * hd, SEED, 995 + i) for i in range(3))
+    lim = o.t2i_limits(M, TEXT, 0)
+    one = lambda: o.attention(q, k_, v, lim, M, M, CFG["heads"], prescale_rows=TEXT)  # noqa
+    med, ts = _median_ms(lambda: (one(), one()), runs)  # batch 2
+    res["sdpa_b2_4352"] = {"median_ms": med}
+    lin_ms = sum(v_["median_ms"] for v_ in sweep.values())
+    step = CFG["layers"] * (BATCH * lin_ms + med)
+    return {"value": step, "unit": "ms/step", "cores": L.qo_num_threads(), "kind": "port",
+            "sample": f"BASELINE configs[0]-[2] on the CPU oracle, 1 warm-up + median of {runs}: "
+                      f"the block at 320 rows, the 4 linears at M={M}, the B2x24h SDPA at "
+                      f"{M} rows; value = {CFG['layers']} x ({BATCH} x linears + SDPA)",
+            "configs": res}
 
 
 def profile_kernel(qd, gpu, reps=5):
     """Launch-only mode for rocprofv3 --pmc passes: a plain copy of a known
     size (the counter calibration: 256 MiB read + 256 MiB written), then
-    the dominant GEMM `reps` times. Nothing is timed or printed as a
-    result."""
+    the dominant GEMM -- the down projection, M=8704 K=12288 N=3072, on the
+    widened int8 weight with the residual-gate epilogue -- `reps` times.
+    Nothing is timed or printed as a result."""
     H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
     L = qd.lib()
     copy_elems = 128 << 20  # bf16: 256 MiB
@@ -176,15 +265,32 @@ def profile_kernel(qd, gpu, reps=5):
     for _ in range(3):
         gpu.check(L.qw_gpu_copy_rows(gpu.h, dst.h, 0, 4096, src.h, 0, 4096,
                                      copy_elems // 4096, 4096), "copy")
-    a = gpu.new(M * H, qd.BF16)
-    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, a.h, 0, M * H, 1, 1, 1.0, 0.0), "fill")
-    wb, q, s = gpu.new(F * H, qd.BF16), gpu.new(F * H, qd.I8), gpu.new(F, qd.F32)
+    a = gpu.new(M * F, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, a.h, 0, M * F, 1, 1, 1.0, 0.0), "fill")
+    wb, q, s = gpu.new(F * H, qd.BF16), gpu.new(F * H, qd.I8), gpu.new(H, qd.F32)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, wb.h, 0, F * H, 1, 2, 0.02, 0.0), "fill")
-    gpu.check(L.h3_gpu_quantize_weight_int8(gpu.h, q.h, s.h, wb.h, F, H), "quant")
+    gpu.check(L.h3_gpu_quantize_weight_int8(gpu.h, q.h, s.h, wb.h, H, F), "quant")
     gpu.check(L.qw_gpu_widen_int8_bf16(gpu.h, wb.h, q.h, F * H), "widen")
-    out = gpu.new(M * F, qd.BF16)
+    ep = epilogue_operands(qd, gpu, M, TEXT + GH * GW)
+    out = gpu.new(M * H, qd.BF16)
     for _ in range(reps):
-        gpu.linear(out, a, wb, M, H, F, wscale=s, epilogue=qd.LINEAR_GELU)
+        gpu.linear(out, a, wb, M, F, H, wscale=s, epilogue=qd.LINEAR_GATE,
+                   **ep[qd.LINEAR_GATE])
+    gpu.submit()
+
+
+def profile_attention(qd, gpu, reps=5):
+    """Launch-only mode for rocprofv3 --pmc: the step's attention call
+    (batch 2 x 24 heads x 4352 rows over the fused q|k|v buffer, text rows
+    attending the text prefix) `reps` times."""
+    H, M, R = CFG["hidden"], BATCH * (TEXT + GH * GW), TEXT + GH * GW
+    L = qd.lib()
+    qkv = gpu.new(M * 3 * H, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, qkv.h, 0, M * 3 * H, 1, 3, 1.0, 0.0), "fill")
+    att = gpu.new(M * H, qd.BF16)
+    for _ in range(reps):
+        gpu.attention(att, qkv, qkv, qkv, BATCH, R, R, CFG["heads"], 3 * H, 3 * H, 3 * H, H, 0,
+                      H, 2 * H, text_rows=TEXT, text_causal=0)
     gpu.submit()
 
 
@@ -290,8 +396,10 @@ def main():
     ap.add_argument("--no-breakdown", action="store_true")
     ap.add_argument("--no-denoise", action="store_true",
                     help="skip the 8-step 512x512 denoise-loop measurement")
-    ap.add_argument("--profile-kernel", action="store_true",
-                    help="only launch a calibration copy and the dominant GEMM (for --pmc)")
+    ap.add_argument("--profile-kernel", nargs="?", const="down", default=None,
+                    choices=["down", "attention"],
+                    help="only launch a calibration copy and the dominant GEMM (default) or "
+                         "the attention kernel, for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
@@ -301,7 +409,7 @@ def main():
     qd = load_qdit()
     gpu = qd.Gpu()
     if args.profile_kernel:
-        profile_kernel(qd, gpu)
+        (profile_attention if args.profile_kernel == "attention" else profile_kernel)(qd, gpu)
         gpu.close()
         return
     R, I = TEXT + GH * GW, GH * GW
@@ -338,17 +446,24 @@ def main():
     lin, sdpa, extra = flops(CFG, R, TEXT, BATCH)
     total_tflops = (lin + sdpa + extra) / ms_step / 1e9
     brk = {} if args.no_breakdown else kernel_breakdown(qd, gpu)
-    up = brk.get("up")
+    down = brk.get("down")
     roofline = None
-    if up:
-        fl = 2.0 * up["M"] * up["N"] * up["K"]
-        achieved = fl / up["gemm_ms"] / 1e9
+    if down:
+        # the dominant kernel of the step (largest total time in the kernel
+        # trace): the down projection's GEMM
+        fl = 2.0 * down["M"] * down["N"] * down["K"]
+        achieved = fl / down["gemm_ms"] / 1e9
         roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
                     "traffic": measured_traffic(),
-                    "kernel": "qw_gemm_bf16_gelu_d (up-projection, M=8704 K=3072 N=12288, "
-                              "int8 weight widened by qw_widen_i8_bf16, scale in the epilogue)",
-                    "flop_per_launch": fl, "ms_per_launch": up["gemm_ms"]}
+                    "kernel": "qw_gemm_bf16_gate_d (down projection, M=8704 K=12288 N=3072, "
+                              "int8 weight widened by qw_widen_i8_bf16, scale and residual "
+                              "gate in the epilogue)",
+                    "flop_per_launch": fl, "ms_per_launch": down["gemm_ms"],
+                    "algorithmic_bytes_per_launch": 2.0 * (down["M"] * down["K"] +
+                                                            down["N"] * down["K"] +
+                                                            2 * down["M"] * down["N"])}
+    sweep = None if args.no_breakdown else sweep_4352(qd, gpu)
     den = None if args.no_breakdown or args.no_denoise else denoise_512(qd, gpu)
     ti2i = None if args.no_breakdown or args.no_denoise else ti2i_1024(qd, gpu, dit)
     cpu = None if args.no_cpu else cpu_baseline()
@@ -366,6 +481,7 @@ def main():
         "step_frac_peak": total_tflops / PEAK_BF16_TFLOPS,
         "flop_per_step": {"linear": lin, "sdpa": sdpa, "other": extra},
         "breakdown": brk,
+        "sweep_4352_bf16": sweep,
         "denoise_512_8step": den,
         "ti2i_1024_one_condition": ti2i,
         "roofline": roofline,
