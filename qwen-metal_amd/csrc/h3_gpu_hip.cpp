@@ -27,7 +27,8 @@ enum {
     K_REORDER, K_FILL, K_QUANT, K_DEQUANT, K_COPY2D, K_ATTN,
     /* GEMM kernels in QW_LINEAR_* epilogue order (store, gelu, gate, qknorm) */
     K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_GEMM_I8_QKN_W8,
-    K_GEMM_BF16_STORE_D, K_GEMM_BF16_GELU_D, K_GEMM_BF16_GATE_D, K_GEMM_BF16_QKN_D, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
+    K_GEMM_BF16_STORE_D, K_GEMM_BF16_GELU_D, K_GEMM_BF16_GATE_D, K_GEMM_BF16_QKN_D,
+    K_GEMM_BF16_STORE_Q, K_GEMM_BF16_GELU_Q, K_GEMM_BF16_GATE_Q, K_GEMM_BF16_QKN_Q, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
     K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_ZERO, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
@@ -37,6 +38,7 @@ static const char *k_names[K_COUNT] = {
     "qw_dequant_int8_f32", "qw_copy2d", "qw_attention_bf16",
     "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8", "qw_gemm_i8_qkn_w8",
     "qw_gemm_bf16_store_d", "qw_gemm_bf16_gelu_d", "qw_gemm_bf16_gate_d", "qw_gemm_bf16_qkn_d",
+    "qw_gemm_bf16_store_q", "qw_gemm_bf16_gelu_q", "qw_gemm_bf16_gate_q", "qw_gemm_bf16_qkn_q",
     "qw_widen_i8_bf16",
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16",
     "qw_gemv_bf16_store", "qw_gemv_bf16_gelu", "qw_gemv_i8_store", "qw_gemv_i8_gelu",
@@ -974,8 +976,19 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     /* bf16 weights (or int8 widened above): the 16x16x32-MFMA kernels;
      * int8 weights with few rows: the kernels that widen in their K loop */
     const int qkn = d->epilogue == QW_LINEAR_QKNORM;
-    const int kid = (int8 && !widen ? K_GEMM_I8_STORE_W8 : K_GEMM_BF16_STORE_D) + d->epilogue;
-    const unsigned threads = 512, bm = 256, bn = 256;
+    /* bf16 weights (or int8 widened above): the 4-wave kernels (one wave
+     * per SIMD, 128 x 128 per wave) for the GELU epilogue and for plain
+     * stores with K >= 4096, the 8-wave kernels otherwise. Same box,
+     * alternating, us, 8-wave / 4-wave: QKV 470-475 / 484-488, out 157-158
+     * / 160-162, up (GELU) 552-565 / 533-540, down 620-632 / 624-630,
+     * 8192^3 765-779 / 720-736. */
+    const int useq = !(int8 && !widen) &&
+                     (d->epilogue == QW_LINEAR_GELU ||
+                      (d->epilogue == QW_LINEAR_STORE && d->k >= 4096));
+    const int kid = (int8 && !widen ? K_GEMM_I8_STORE_W8
+                                    : (useq ? K_GEMM_BF16_STORE_Q : K_GEMM_BF16_STORE_D)) +
+                    d->epilogue;
+    const unsigned threads = useq ? 256 : 512, bm = 256, bn = 256;
     a.norm_q = qkn ? (const uint16_t *)d->norm_q->ptr : NULL;
     a.norm_k = qkn ? (const uint16_t *)d->norm_k->ptr : NULL;
     a.rope_cos = qkn ? (const float *)d->rope_cos->ptr : NULL;

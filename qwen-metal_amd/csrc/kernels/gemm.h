@@ -192,12 +192,11 @@ __device__ __forceinline__ void gemm_tile(const qw_gemm_args &a, uint32_t &tm, u
  * instead of 16-byte pieces, and the residual/gate reads of the GATE
  * epilogue are coalesced the same way. A lane keeps the same 8 columns for
  * every row, so it loads their scale and bias once. */
-template <int EPI, int INT8, int MI, int NI, int MF = 32>
-__device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx16 (&acc)[NI][MI],
+template <int EPI, int INT8, int MI, int NI, class SlabWriter>
+__device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, SlabWriter write_slab,
                                                   float *region, uint32_t row0, uint32_t col0,
-                                                  uint32_t h, uint32_t i32, uint32_t lane,
-                                                  float *pst, const float *pld, uint32_t npart,
-                                                  uint32_t own) {
+                                                  uint32_t lane, float *pst, const float *pld,
+                                                  uint32_t npart, uint32_t own) {
 #pragma clang fp contract(off)
     constexpr uint32_t LDF = NI * 32 + 4; /* floats per staged row */
     const bool scaled = INT8 || a.wscale != nullptr;
@@ -243,28 +242,7 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, floatx1
     const uint32_t swap = (cc >> 3) & 1;
 #pragma unroll
     for (int mi = 0; mi < MI; mi++) {
-        if constexpr (MF == 16) { /* quarter 2p + q: rows 16 q + l % 16, cols 16 p + 4 (l / 16) */
-#pragma unroll
-            for (int ni = 0; ni < NI; ni++)
-#pragma unroll
-                for (int p = 0; p < 2; p++)
-#pragma unroll
-                    for (int q = 0; q < 2; q++) {
-                        const int k = 2 * p + q;
-                        *(floatx4 *)(region + (16 * q + (lane & 15)) * LDF + ni * 32 + 16 * p +
-                                     4 * (lane >> 4)) =
-                            floatx4{acc[ni][mi][4 * k], acc[ni][mi][4 * k + 1],
-                                    acc[ni][mi][4 * k + 2], acc[ni][mi][4 * k + 3]};
-                    }
-        } else {
-#pragma unroll
-            for (int ni = 0; ni < NI; ni++)
-#pragma unroll
-                for (int g = 0; g < 4; g++)
-                    *(floatx4 *)(region + i32 * LDF + ni * 32 + 8 * g + 4 * h) =
-                        floatx4{acc[ni][mi][4 * g], acc[ni][mi][4 * g + 1], acc[ni][mi][4 * g + 2],
-                                acc[ni][mi][4 * g + 3]};
-        }
+        write_slab(mi); /* fp32 sums of rows [32 mi, 32 mi + 32) into region */
 #pragma unroll
         for (int p = 0; p < 8; p++) {
             const uint32_t lr = 4 * p + rr;
@@ -871,7 +849,32 @@ __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char
         /* split-tile partials: row-major 256 x 256 fp32 */
         static_assert(S::BN == 256 && S::BM * S::BN <= QW_SPLIT_PART, "partial tile size");
         const uint32_t poff = wm * (MI * 32) * 256 + wn * (NI * 32);
-        gemm_epilogue_lds<EPI, INT8, MI, NI, MF>(a, acc, region, row0, col0, h, i32, lane,
+        constexpr uint32_t LDF = NI * 32 + 4; /* floats per staged row */
+        auto write_slab = [&](int mi) __attribute__((always_inline)) {
+            if constexpr (MF == 16) { /* quarter 2p + q: rows 16 q + l % 16, cols 16 p + 4 (l / 16) */
+#pragma unroll
+                for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+                    for (int p = 0; p < 2; p++)
+#pragma unroll
+                        for (int q = 0; q < 2; q++) {
+                            const int k = 2 * p + q;
+                            *(floatx4 *)(region + (16 * q + (lane & 15)) * LDF + ni * 32 + 16 * p +
+                                         4 * (lane >> 4)) =
+                                floatx4{acc[ni][mi][4 * k], acc[ni][mi][4 * k + 1],
+                                        acc[ni][mi][4 * k + 2], acc[ni][mi][4 * k + 3]};
+                        }
+            } else {
+#pragma unroll
+                for (int ni = 0; ni < NI; ni++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++)
+                        *(floatx4 *)(region + i32 * LDF + ni * 32 + 8 * g + 4 * h) =
+                            floatx4{acc[ni][mi][4 * g], acc[ni][mi][4 * g + 1],
+                                    acc[ni][mi][4 * g + 2], acc[ni][mi][4 * g + 3]};
+            }
+        };
+        gemm_epilogue_lds<EPI, INT8, MI, NI>(a, write_slab, region, row0, col0, lane,
                                              pst ? pst + poff : nullptr, pld ? pld + poff : nullptr,
                                              npart, own);
     }

@@ -1,0 +1,256 @@
+/* bf16 GEMM with one wave per SIMD: a 256 x 256 tile per workgroup of 4
+ * waves (2 x 2), each wave a 128 x 128 block of 8 x 8 v_mfma_f32_16x16x32_bf16
+ * tiles whose 64 accumulators (256 fp32 per lane) sit in the accumulation
+ * registers. Against the 8-wave tile (4 x 2 waves of 64 x 128) it reads a
+ * third fewer operand bytes from LDS per MFMA -- each wave's fragments
+ * serve 128 rows and 128 columns instead of 64 and 128 -- which is the
+ * resource the 8-wave main loop runs out of; each sub-step of 32 k is 64
+ * independent MFMAs (1024 matrix-pipe cycles) under which its 16 fragment
+ * reads and the next K-slice's 16 direct loads are issued.
+ *
+ * Operands, LDS layout, swizzle, direct-to-LDS loads, the held-back
+ * sub-step across each K-slice barrier, tile walk, split tiles and the
+ * LDS-staged epilogue are those of gemm.h; only the wave geometry and the
+ * accumulator arrays differ. out[m, n] = epi(sum_k A[m, k] W[n, k]). */
+#pragma once
+#include "gemm.h"
+
+#define QG_A_BYTES (256 * 128) /* 256 rows x 64 bf16 */
+#define QG_STAGE (2 * QG_A_BYTES)
+
+struct QgCtx {
+    u32x4 a_rs4, w_rs4;
+    uint32_t a_dvoff[8], w_dvoff[8];
+    uint32_t dst0;           /* this wave's 64-row share of a stage */
+    uint32_t a_frag, w_frag; /* fragment row base (rows + lane % 16) in bytes */
+    uint32_t ch[2];          /* swizzled 16-byte chunk of sub-step 0 / 1 */
+};
+
+/* acc += W-fragment x A-fragment, in place. The accumulator is an operand
+ * tied to the result, so each of the wave's 64 accumulators keeps one set
+ * of accumulation registers for the whole loop (with the compiler builtin
+ * and a fixed interleave the register allocator rotated them through
+ * ordinary registers: hundreds of copies per K-slice). Volatile: the
+ * MFMAs, the direct loads and the fragment reads issue in source order. */
+#define QG_MFMA(acc, w, x) \
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(w), "v"(x))
+
+/* fragment j of a sub-step, in the order its MFMAs consume them (W block 0,
+ * A blocks 0-7, W blocks 1-7) */
+__device__ __forceinline__ void qg_read(const QgCtx &c, const unsigned char *cur, uint32_t ch,
+                                        bf16x8 (&af)[8], bf16x8 (&bw)[8], int j) {
+    if (j == 0)
+        bw[0] = *(const bf16x8 *)(cur + QG_A_BYTES + c.w_frag + ch);
+    else if (j <= 8)
+        af[j - 1] = *(const bf16x8 *)(cur + c.a_frag + (j - 1) * 2048 + ch);
+    else
+        bw[j - 8] = *(const bf16x8 *)(cur + QG_A_BYTES + c.w_frag + (j - 8) * 2048 + ch);
+}
+
+/* One 64-k slice: the stage `cur` is multiplied while slice k_next streams
+ * into `nxt`. The slice's second sub-step is held back (its fragments in
+ * pa, pw) and runs at the start of the next slice, after the barrier, while
+ * that slice's direct loads and first fragments are issued: one direct load
+ * and one fragment read every 4 MFMAs; under the 64 MFMAs of sub-step 0 the
+ * 16 fragments of sub-step 1 are read, one every 4 MFMAs. */
+template <bool PREV>
+__device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], bf16x8 (&pa)[8],
+                                         bf16x8 (&pw)[8], const unsigned char *__restrict__ cur,
+                                         unsigned char *__restrict__ nxt, uint32_t k_next) {
+    const uint32_t nl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)nxt;
+    auto dma = [&](int j) __attribute__((always_inline)) {
+        if (j < 8)
+            gemm_dma16(c.a_rs4, nl + c.dst0 + j * 1024, c.a_dvoff[j], k_next * 2);
+        else
+            gemm_dma16(c.w_rs4, nl + QG_A_BYTES + c.dst0 + (j - 8) * 1024, c.w_dvoff[j - 8],
+                       k_next * 2);
+    };
+    /* (one direct load and one fragment read every 4 MFMAs measured 7-10%
+     * faster than the 16 direct loads issued back to back, than the loads
+     * spread over both sub-steps, and than the read placed before the
+     * load) */
+    bf16x8 af[8], bw[8], af1[8], bw1[8];
+    if (PREV) {
+#pragma unroll
+        for (int i = 0; i < 64; i++) {
+            QG_MFMA(acc[i & 7][i >> 3], pw[i >> 3], pa[i & 7]);
+            if ((i & 3) == 1) dma(i >> 2);
+            if ((i & 3) == 3) qg_read(c, cur, c.ch[0], af, bw, i >> 2);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 16; j++) dma(j);
+#pragma unroll
+        for (int j = 0; j < 16; j++) qg_read(c, cur, c.ch[0], af, bw, j);
+    }
+#pragma unroll
+    for (int i = 0; i < 64; i++) {
+        QG_MFMA(acc[i & 7][i >> 3], bw[i >> 3], af[i & 7]);
+        if ((i & 3) == 3) qg_read(c, cur, c.ch[1], af1, bw1, i >> 2);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) pa[i] = af1[i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) pw[i] = bw1[i];
+}
+
+/* Sums of tile (tm, tn) over k-steps [kb, ke) into acc; ends with the LDS
+ * stages free (after a barrier). */
+__device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char *lds,
+                                            unsigned char *lds_b, uint32_t tm, uint32_t tn,
+                                            uint32_t kb, uint32_t ke, floatx4 (&acc)[8][8]) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    const uint32_t m0 = tm * 256, n0 = tn * 256;
+    QgCtx c;
+    const uint32_t lrow = lane >> 3, lp = lane & 7;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t r = wave * 64 + j * 8 + lrow;
+        c.a_dvoff[j] = (min(m0 + r, a.m - 1) * a.lda + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+        c.w_dvoff[j] = (min(n0 + r, a.n - 1) * a.k + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+    }
+    c.a_rs4 = gemm_rs4(a.a, a.a_bytes);
+    c.w_rs4 = gemm_rs4(a.w, a.w_bytes);
+    c.dst0 = wave * 64 * 128;
+    const uint32_t l16 = lane & 15, h = lane >> 4, swz = (l16 >> 1) & 7u;
+    c.a_frag = (wm * 128 + l16) * 128;
+    c.w_frag = (wn * 128 + l16) * 128;
+    c.ch[0] = ((0 + h) ^ swz) << 4;
+    c.ch[1] = ((4 + h) ^ swz) << 4;
+#pragma unroll
+    for (int mb = 0; mb < 8; mb++)
+#pragma unroll
+        for (int nb = 0; nb < 8; nb++) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t KT = ke;
+    {
+        const uint32_t nb =
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)lds;
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            gemm_dma16(c.a_rs4, nb + c.dst0 + j * 1024, c.a_dvoff[j], kb * GBK * 2);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            gemm_dma16(c.w_rs4, nb + QG_A_BYTES + c.dst0 + j * 1024, c.w_dvoff[j], kb * GBK * 2);
+    }
+    QW_SLICE_END();
+    bf16x8 pa[8], pw[8];
+    qg_slice<false>(c, acc, pa, pw, lds, lds_b, (kb + 1 < KT ? kb + 1 : kb) * GBK);
+    QW_SLICE_END();
+    uint32_t kt = kb + 1;
+    for (; kt + 1 < KT; kt += 2) {
+        qg_slice<true>(c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
+        QW_SLICE_END();
+        qg_slice<true>(c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
+        QW_SLICE_END();
+    }
+    if (kt < KT) {
+        qg_slice<true>(c, acc, pa, pw, lds_b, lds, kt * GBK);
+        QW_SLICE_END();
+    }
+#pragma unroll
+    for (int i = 0; i < 64; i++) QG_MFMA(acc[i & 7][i >> 3], pw[i >> 3], pa[i & 7]);
+    /* the epilogue reads the accumulators with ordinary instructions: let
+     * the last MFMAs' results land first (the inline assembly hides them
+     * from the compiler's hazard tracking) */
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
+template <int EPI>
+__device__ __forceinline__ void qg_finish(const qw_gemm_args &a, unsigned char *lds,
+                                          unsigned char *lds_b, uint32_t tm, uint32_t tn,
+                                          floatx4 (&acc)[8][8], float *pst = nullptr,
+                                          const float *pld = nullptr, uint32_t npart = 0,
+                                          uint32_t own = 0) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    const uint32_t row0 = tm * 256 + wm * 128, col0 = tn * 256 + wn * 128;
+    constexpr uint32_t LDF = 128 + 4, REG = 32 * LDF * 4;
+    /* waves 0, 1 stage through `lds`, 2, 3 through `lds_b` (free after the
+     * loop's last barrier), one 32-row slab (16.5 KB) at a time */
+    float *region = (float *)((wave < 2 ? lds : lds_b) + (wave & 1) * REG);
+    const uint32_t poff = wm * 128 * 256 + wn * 128;
+    /* slab mi: rows 32 mi + 16 q + lane % 16 (tile mb = 2 mi + q), columns
+     * 32 ni + 16 p + 4 (lane / 16) + 0..3 (tile nb = 2 ni + p) */
+    auto write_slab = [&](int mi) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ni = 0; ni < 4; ni++)
+#pragma unroll
+            for (int p = 0; p < 2; p++)
+#pragma unroll
+                for (int q = 0; q < 2; q++)
+                    *(floatx4 *)(region + (16 * q + (lane & 15)) * LDF + ni * 32 + 16 * p +
+                                 4 * (lane >> 4)) = acc[2 * mi + q][2 * ni + p];
+    };
+    gemm_epilogue_lds<EPI, 0, 4, 4>(a, write_slab, region, row0, col0, lane,
+                                    pst ? pst + poff : nullptr, pld ? pld + poff : nullptr, npart,
+                                    own);
+}
+
+template <int EPI>
+__device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *lds,
+                                        unsigned char *lds_b) {
+    const uint32_t KT = a.k / GBK;
+    const uint32_t nt = a.tiles_m * a.tiles_n;
+    const bool split = a.split > 1;
+    const uint32_t ndp = split ? a.dp_tiles : nt;
+    floatx4 acc[8][8];
+    uint32_t pid = blockIdx.x, tm, tn;
+    if (pid < ndp) {
+        if (!split) {
+            /* one workgroup per CU walks the tiles in strides of the grid;
+             * id and id + grid sit on the same XCD (grid % 8 == 0) */
+            for (uint32_t id = pid; id < ndp; id += gridDim.x) {
+                uint32_t q = id;
+                if ((ndp & 7u) == 0) q = (q & 7u) * (ndp >> 3) + (q >> 3);
+                gemm_tile_at(a, q, tm, tn);
+                qg_mainloop(a, lds, lds_b, tm, tn, 0, KT, acc);
+                qg_finish<EPI>(a, lds, lds_b, tm, tn, acc);
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            }
+            return;
+        }
+        if ((ndp & 7u) == 0) pid = (pid & 7u) * (ndp >> 3) + (pid >> 3);
+        gemm_tile_at(a, pid, tm, tn);
+        qg_mainloop(a, lds, lds_b, tm, tn, 0, KT, acc);
+        qg_finish<EPI>(a, lds, lds_b, tm, tn, acc);
+        return;
+    }
+    /* piece of a split tile (k-range-major numbering, as gemm.h) */
+    __shared__ uint32_t ticket;
+    const uint32_t R = nt - ndp, S = a.split, np = R * S;
+    uint32_t q = pid - ndp;
+    if ((np & 7u) == 0) q = (q & 7u) * (np >> 3) + (q >> 3);
+    const uint32_t piece = q / R, r = q % R;
+    const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
+    gemm_tile_at(a, ndp + r, tm, tn);
+    qg_mainloop(a, lds, lds_b, tm, tn, kb, ke, acc);
+    float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
+    qg_finish<EPI>(a, lds, lds_b, tm, tn, acc, slots + (size_t)piece * QW_SPLIT_PART);
+    __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the partial's stores are done */
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        ticket = __hip_atomic_fetch_add(a.sk_flag + r, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (ticket != S - 1) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    qg_finish<EPI>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S, piece);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.sk_flag + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+#define QG_ENTRY(name, EPI)                                                                    \
+    QW_KERNEL void __launch_bounds__(256, 1) name(qw_gemm_args a) {                            \
+        __shared__ __attribute__((aligned(16))) unsigned char lds[QG_STAGE];                    \
+        __shared__ __attribute__((aligned(16))) unsigned char lds_b[QG_STAGE];                  \
+        qg_impl<EPI>(a, lds, lds_b);                                                           \
+    }
+
+QG_ENTRY(qw_gemm_bf16_store_q, QW_EPI_STORE)
+QG_ENTRY(qw_gemm_bf16_gelu_q, QW_EPI_GELU)
+QG_ENTRY(qw_gemm_bf16_gate_q, QW_EPI_GATE)
+QG_ENTRY(qw_gemm_bf16_qkn_q, QW_EPI_QKNORM)

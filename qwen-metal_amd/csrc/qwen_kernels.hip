@@ -3,5 +3,6 @@
 #include "kernels/common.h"
 #include "kernels/elementwise.h"
 #include "kernels/gemm.h"
+#include "kernels/gemm_q.h"
 #include "kernels/attention.h"
 #include "kernels/lora.h"

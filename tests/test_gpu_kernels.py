@@ -171,6 +171,9 @@ SPLIT_CASES = [
     (300, 8192, 1032, True, "gelu"),
     (512, 4096, 2048, False, "gate"),
     (256, 12288, 3072, False, "store"),
+    # bf16 GELU and K >= 4096 stores run the 4-wave (one wave per SIMD)
+    # kernels: their split-tile path
+    (512, 8192, 2048, False, "gelu"),
 ]
 
 
