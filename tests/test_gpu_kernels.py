@@ -174,6 +174,8 @@ SPLIT_CASES = [
     # bf16 GELU and K >= 4096 stores run the 4-wave (one wave per SIMD)
     # kernels: their split-tile path
     (512, 8192, 2048, False, "gelu"),
+    # int8 weights at >= 512 rows: widened first, then the bf16 kernels
+    (512, 8192, 2048, True, "gate"),
 ]
 
 
