@@ -27,7 +27,6 @@ enum {
     K_REORDER, K_FILL, K_QUANT, K_DEQUANT, K_COPY2D, K_ATTN,
     /* GEMM kernels in QW_LINEAR_* epilogue order (store, gelu, gate, qknorm) */
     K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_GEMM_I8_QKN_W8,
-    K_GEMM_BF16_STORE_D, K_GEMM_BF16_GELU_D, K_GEMM_BF16_GATE_D, K_GEMM_BF16_QKN_D,
     K_GEMM_BF16_STORE_Q, K_GEMM_BF16_GELU_Q, K_GEMM_BF16_GATE_Q, K_GEMM_BF16_QKN_Q, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
     K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_ZERO, K_COUNT
 };
@@ -37,7 +36,6 @@ static const char *k_names[K_COUNT] = {
     "qw_modulation_reorder_bf16", "qw_fill_normal_bf16", "qw_quantize_int8_rows",
     "qw_dequant_int8_f32", "qw_copy2d", "qw_attention_bf16",
     "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8", "qw_gemm_i8_qkn_w8",
-    "qw_gemm_bf16_store_d", "qw_gemm_bf16_gelu_d", "qw_gemm_bf16_gate_d", "qw_gemm_bf16_qkn_d",
     "qw_gemm_bf16_store_q", "qw_gemm_bf16_gelu_q", "qw_gemm_bf16_gate_q", "qw_gemm_bf16_qkn_q",
     "qw_widen_i8_bf16",
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16",
@@ -820,8 +818,11 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
  * all of them when there is no full wave), each of its tiles can instead be
  * cut into s k-ranges: R s pieces taking ceil(R s / cus) waves of 1/s the
  * length. s minimises that tail time plus 0.02 (s - 1) for writing and
- * re-reading the fp32 partials, and is used only when that beats 0.9 of the
- * whole-tile tail. Pieces stay at least 32 k-steps (2048 k) long: shorter
+ * re-reading the fp32 partials, and is used only when that beats half of
+ * the whole-tile tail: a split tail costs more than its piece count
+ * suggests (M = 8704, K = 12288, N = 3072: 152 tail tiles in 3 pieces
+ * 565 us against 530 us for the whole-tile walk; M = 6144, 32 tail tiles
+ * in 6 pieces 438 against 494). Pieces stay at least 32 k-steps (2048 k) long: shorter
  * pieces lost more to their partials than they gained (K = 3072 linears
  * measured slower when split, K = 12288 ones faster), and
  * R s <= QW_SPLIT_MAX_PIECES * cus bounds the partial workspace. */
@@ -830,9 +831,8 @@ static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps,
                              uint64_t max_pieces = (uint64_t)QW_SPLIT_MAX_PIECES * 1024u) {
     const uint32_t min_steps = 32;
     const uint32_t G = g->cus, R = tiles % G;
-    if (R == 0) return 1;
     uint32_t best = 1;
-    double best_t = 0.9;
+    double best_t = 0.5;
     for (uint32_t s = 2; s <= 8; s++) {
         if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * G || (uint64_t)R * s > max_pieces ||
             ksteps < min_steps * s)
@@ -968,26 +968,23 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     {
         const uint64_t ab = ((uint64_t)(d->rows - 1) * d->lda + d->k) * 2;
         const uint64_t wb = (uint64_t)d->cols * d->k * (int8 && !widen ? 1 : 2);
-        if (ab >= (1ull << 31) || wb >= (1ull << 31))
+        const uint64_t ob = ((uint64_t)(d->rows - 1) * d->ldc + d->cols) * 2;
+        if (ab >= (1ull << 31) || wb >= (1ull << 31) || ob >= (1ull << 31))
             return fail(g, "linear: operand exceeds 2 GiB buffer range");
         a.a_bytes = (uint32_t)ab;
         a.w_bytes = (uint32_t)wb;
+        a.out_bytes = (uint32_t)ob;
     }
     /* bf16 weights (or int8 widened above): the 16x16x32-MFMA kernels;
      * int8 weights with few rows: the kernels that widen in their K loop */
     const int qkn = d->epilogue == QW_LINEAR_QKNORM;
     /* bf16 weights (or int8 widened above): the 4-wave kernels (one wave
-     * per SIMD, 128 x 128 per wave) for the GELU epilogue and for plain
-     * stores with K >= 4096, the 8-wave kernels otherwise. Same box,
-     * alternating, us, 8-wave / 4-wave: QKV 470-475 / 484-488, out 157-158
-     * / 160-162, up (GELU) 552-565 / 533-540, down 620-632 / 624-630,
-     * 8192^3 765-779 / 720-736. */
-    const int useq = !(int8 && !widen) &&
-                     (d->epilogue == QW_LINEAR_GELU ||
-                      (d->epilogue == QW_LINEAR_STORE && d->k >= 4096));
-    const int kid = (int8 && !widen ? K_GEMM_I8_STORE_W8
-                                    : (useq ? K_GEMM_BF16_STORE_Q : K_GEMM_BF16_STORE_D)) +
-                    d->epilogue;
+     * per SIMD, 128 x 128 per wave). Same box, alternating, M = 8704, us,
+     * against the 8-wave 16x16x32 kernels they replaced (two waves per
+     * SIMD, 64 x 128 per wave): QKV 447 / 458, out 149 / 155, up (GELU)
+     * 537 / 554, down 598 / 623. */
+    const int useq = !(int8 && !widen);
+    const int kid = (useq ? K_GEMM_BF16_STORE_Q : K_GEMM_I8_STORE_W8) + d->epilogue;
     const unsigned threads = useq ? 256 : 512, bm = 256, bn = 256;
     a.norm_q = qkn ? (const uint16_t *)d->norm_q->ptr : NULL;
     a.norm_k = qkn ? (const uint16_t *)d->norm_k->ptr : NULL;
@@ -1047,6 +1044,10 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
                 }
             }
             const uint32_t R = tiles % g->cus;
+            /* the workspace holds QW_SPLIT_MAX_PIECES * cus partials and
+             * cus counters; split_choice keeps within both */
+            if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * g->cus || R > g->cus)
+                return fail(g, "linear: %u x %u split pieces exceed the partial workspace", R, s);
             a.dp_tiles = tiles - R;
             a.split = s;
             a.sk_part = g->sk_part;
@@ -1058,7 +1059,7 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * the tiles, so a tile's output stores drain under the next tile's first
      * loads (up 521 -> 514 us, QKV 365 -> 359 us against one workgroup per
      * tile) */
-    if (kid >= K_GEMM_BF16_STORE_D && a.split == 1 && grid > g->cus && g->cus % 8 == 0)
+    if (useq && a.split == 1 && grid > g->cus && g->cus % 8 == 0)
         grid = g->cus;
     return launch(g, kid, dim3(grid), dim3(threads), a);
 }

@@ -8,10 +8,11 @@
  * BM = WM * MI * 32, BN = WN * NI * 32, each wave an (MI*32) x (NI*32) block
  * of MI x NI MFMA tiles, stepping K by 64. One geometry is built: 4 x 2
  * waves of 2 x 4 blocks (256 x 256, two waves per SIMD, 128 accumulators
- * each: one wave's MFMAs cover the other's LDS/global latency). bf16
- * weights use v_mfma_f32_16x16x32_bf16 (each 32 x 32 block as four 16 x 16
- * blocks, the "_d" kernels); int8 weights widened in the loop use
- * v_mfma_f32_32x32x16_bf16 (the "_w8" kernels).
+ * each: one wave's MFMAs cover the other's LDS/global latency), with
+ * v_mfma_f32_32x32x16_bf16, for int8 weights widened in the loop (the
+ * "_w8" kernels). bf16 weights run on the 4-wave kernels of gemm_q.h,
+ * which share this file's LDS layout, direct loads, tile order and
+ * epilogue.
  * A and W tiles are staged through LDS, double-buffered (2 x 64 KB at
  * 256 x 256), with the next K-slice's global loads in flight while the
  * current one is multiplied; within a K-slice the operand fragments of
@@ -32,6 +33,10 @@
 #include "common.h"
 
 #define GBK 64
+/* epilogue rows per pass: 8-wave kernels (two waves per SIMD share its registers) */
+#ifndef QW_EPI_RP_D
+#define QW_EPI_RP_D 2
+#endif
 /* End of a K-slice of the 16x16x32 pipeline: its direct loads landed
  * (vmcnt(0)) and this wave's LDS reads done, then a bare s_barrier. The
  * direct loads are issued from inline assembly, so the compiler's own wait
@@ -41,6 +46,8 @@
 #define QW_SPLIT_PART (256u * 256u)
 /* buffer cache policy sc0 | sc1: coherent at device scope */
 #define QW_CPOL_COHERENT 17
+/* buffer cache policy nt: non-temporal */
+#define QW_CPOL_NT 2
 
 __device__ __forceinline__ uint32_t g_swz(uint32_t row, uint32_t chunk) {
     return row * 128u + ((chunk ^ ((row >> 1) & 7u)) << 4);
@@ -183,53 +190,68 @@ __device__ __forceinline__ void gemm_tile(const qw_gemm_args &a, uint32_t &tm, u
     gemm_tile_at(a, pid, tm, tn);
 }
 
-/* Epilogue through LDS: the same arithmetic as gemm_epilogue, but the
- * fp32 sums of each 32-row slab of the wave's block are first written to a
- * wave-private LDS region (row stride NI*32 + 4 floats: the 16 lanes of a
- * ds_write_b128 pass land on 16 distinct 4-bank groups), then read back
- * row-contiguous: 16 lanes per row, 8 columns (one 16-byte global store)
- * per lane, so every output row segment is written by whole 256-byte runs
- * instead of 16-byte pieces, and the residual/gate reads of the GATE
+/* Epilogue through LDS: the fp32 sums of each 32-row slab of the wave's
+ * block are first written to a wave-private LDS region (row stride
+ * NI*32 + 4 floats: the 16 lanes of a ds_write_b128 pass land on 16
+ * distinct 4-bank groups), then read back row-contiguous: 16 lanes per row,
+ * 8 columns (one 16-byte store) per lane, so every output row segment is
+ * written by whole 256-byte runs, and the residual/gate reads of the GATE
  * epilogue are coalesced the same way. A lane keeps the same 8 columns for
- * every row, so it loads their scale and bias once. */
-template <int EPI, int INT8, int MI, int NI, class SlabWriter>
-__device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, SlabWriter write_slab,
-                                                  float *region, uint32_t row0, uint32_t col0,
-                                                  uint32_t lane, float *pst, const float *pld,
-                                                  uint32_t npart, uint32_t own) {
+ * every row, so it loads their scale and bias once.
+ *
+ * Rows are processed RP at a time without branches: a lane outside the
+ * output (row >= m, or its columns >= n) addresses its output and residual
+ * past the end of a buffer resource, so its loads return zeros and its
+ * stores are dropped. The per-row operands of the RP rows (residual, gate,
+ * RoPE table rows) are issued before their LDS reads, so the rows' memory
+ * latencies overlap each other instead of adding up row by row.
+ *
+ * MODE 0: a finished tile. MODE 1: a piece of a split tile, whose fp32 sums
+ * are stored to its partial slot. MODE 2: the last piece of a split tile,
+ * which adds all pieces' sums in piece order (its own from LDS) and runs
+ * the epilogue. */
+template <int EPI, int INT8, int MI, int NI, int RP, int MODE, class SlabWriter>
+__device__ __forceinline__ void gemm_epilogue_mode(const qw_gemm_args &a, SlabWriter write_slab,
+                                                   float *region, uint32_t row0, uint32_t col0,
+                                                   uint32_t lane, float *pst, const float *pld,
+                                                   uint32_t npart, uint32_t own) {
 #pragma clang fp contract(off)
     constexpr uint32_t LDF = NI * 32 + 4; /* floats per staged row */
+    static_assert(8 % RP == 0, "rows per pass");
     const bool scaled = INT8 || a.wscale != nullptr;
     /* split-tile partials go through device-coherent buffer accesses (write
      * through / read past the XCD's L2), so pieces on different XCDs see
      * each other's sums without any L2 write-back or invalidate */
     const __amdgpu_buffer_rsrc_t part_rsrc = __builtin_amdgcn_make_buffer_rsrc(
         (void *)a.sk_part, (short)0, (int)0x7FFFFFF0, 0x00020000);
+    const __amdgpu_buffer_rsrc_t out_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.out, (short)0, (int)a.out_bytes, 0x00020000);
     /* read-back geometry: lane -> (row within a 4-row group, 8-column chunk) */
     const uint32_t rr = lane >> 4, cc = lane & 15;
     constexpr uint32_t CHUNKS = NI * 32 / 8; /* 16 for NI = 4 */
     static_assert(CHUNKS == 16, "read-back maps 16 lanes to one row");
     const uint32_t col = col0 + cc * 8;
-    const bool col_ok = col < a.n; /* n % 8 == 0 */
+    const bool col_ok = col < a.n;                 /* n % 8 == 0 */
+    const uint32_t colc = col_ok ? col : a.n - 8;  /* in-range column for operand loads */
     float sc[8], bias[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) sc[j] = 1.0f, bias[j] = 0.0f;
-    if (col_ok) {
+    if (MODE != 1) {
         if (scaled) {
-            const floatx4 s0 = *(const floatx4 *)(a.wscale + col);
-            const floatx4 s1 = *(const floatx4 *)(a.wscale + col + 4);
+            const floatx4 s0 = *(const floatx4 *)(a.wscale + colc);
+            const floatx4 s1 = *(const floatx4 *)(a.wscale + colc + 4);
 #pragma unroll
             for (int j = 0; j < 4; j++) sc[j] = s0[j], sc[4 + j] = s1[j];
         }
         if (a.bias) {
-            const u32x4 bb = *(const u32x4 *)(a.bias + col);
+            const u32x4 bb = *(const u32x4 *)(a.bias + colc);
 #pragma unroll
             for (int j = 0; j < 4; j++) bias[2 * j] = lo_bf(bb[j]), bias[2 * j + 1] = hi_bf(bb[j]);
         }
     }
     /* QW_EPI_QKNORM: this wave's 128 columns are one head (tiles start at
      * multiples of 256); q or k heads get the norm weight of their kind */
-    const bool qk_head = EPI == QW_EPI_QKNORM && col0 < a.qk_cols;
+    const bool qk_head = EPI == QW_EPI_QKNORM && MODE != 1 && col0 < a.qk_cols;
     float nw[8];
     if (EPI == QW_EPI_QKNORM && qk_head) {
         const u32x4 wn = *(const u32x4 *)((col0 < a.qk_cols / 2 ? a.norm_q : a.norm_k) + 8 * cc);
@@ -240,110 +262,168 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, SlabWri
      * lanes 8-15 of a row start with the upper half, so one ds_read_b128
      * pass covers all 64 banks */
     const uint32_t swap = (cc >> 3) & 1;
+    auto lds_row = [&](uint32_t lr, float (&v)[8]) __attribute__((always_inline)) {
+        const floatx4 v0 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * swap);
+        const floatx4 v1 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * (swap ^ 1));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[j] = swap ? v1[j] : v0[j];
+            v[4 + j] = swap ? v0[j] : v1[j];
+        }
+    };
 #pragma unroll
     for (int mi = 0; mi < MI; mi++) {
         write_slab(mi); /* fp32 sums of rows [32 mi, 32 mi + 32) into region */
 #pragma unroll
-        for (int p = 0; p < 8; p++) {
-            const uint32_t lr = 4 * p + rr;
-            const floatx4 v0 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * swap);
-            const floatx4 v1 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * (swap ^ 1));
-            const uint32_t row = row0 + mi * 32 + lr;
-            /* a 16-lane row group is all in or all out (n % 8 == 0 for the
-             * columns; one row per group), so the QKNORM shuffles stay
-             * within active groups */
-            if (!col_ok || row >= a.m) continue;
-            float y[8];
+        for (int p0 = 0; p0 < 8; p0 += RP) {
+            uint32_t ooff[RP];
+            u32x4 gv[RP], rv[RP];
+            floatx4 rc[RP], rs[RP];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                y[j] = swap ? v1[j] : v0[j];
-                y[4 + j] = swap ? v0[j] : v1[j];
+            for (int i = 0; i < RP; i++) {
+                const uint32_t row = row0 + mi * 32 + 4 * (p0 + i) + rr;
+                ooff[i] = col_ok && row < a.m ? (row * a.ldc + col) * 2 : 0x80000000u;
+                if (EPI == QW_EPI_GATE && MODE != 1) {
+                    const uint32_t mrow = a.row_map[min(row, a.m - 1)];
+                    gv[i] = *(const u32x4 *)(a.gate + (size_t)mrow * a.gate_row_stride + colc);
+                    rv[i] = __builtin_bit_cast(
+                        u32x4, __builtin_amdgcn_raw_buffer_load_b128(out_rsrc, ooff[i], 0, 0));
+                }
             }
-            const uint32_t poff = (mi * 32 + lr) * 256 + cc * 8;
-            if (pst) { /* piece of a split tile: keep the fp32 sums */
-                const uint32_t bo = (uint32_t)((pst - a.sk_part) + poff) * 4;
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    __builtin_bit_cast(u32x4, floatx4{y[0], y[1], y[2], y[3]}), part_rsrc, bo, 0,
-                    QW_CPOL_COHERENT);
-                __builtin_amdgcn_raw_buffer_store_b128(
-                    __builtin_bit_cast(u32x4, floatx4{y[4], y[5], y[6], y[7]}), part_rsrc, bo + 16,
-                    0, QW_CPOL_COHERENT);
+            if (EPI == QW_EPI_QKNORM && qk_head) {
+#pragma unroll
+                for (int i = 0; i < RP; i++) {
+                    const uint32_t row = min(row0 + mi * 32 + 4 * (p0 + i) + rr, a.m - 1);
+                    const size_t t = (size_t)(row % a.rope_rows) * 64 + 4 * cc;
+                    rc[i] = *(const floatx4 *)(a.rope_cos + t);
+                    rs[i] = *(const floatx4 *)(a.rope_sin + t);
+                }
+            }
+            float y[RP][8];
+            if (MODE == 2) { /* all pieces of a split tile, summed in piece order */
+#pragma unroll
+                for (int i = 0; i < RP; i++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) y[i][j] = 0.0f;
+                for (uint32_t pc = 0; pc < npart; pc++) {
+                    if (pc == own) {
+#pragma unroll
+                        for (int i = 0; i < RP; i++) {
+                            float v[8];
+                            lds_row(4 * (p0 + i) + rr, v);
+#pragma unroll
+                            for (int j = 0; j < 8; j++) y[i][j] += v[j];
+                        }
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < RP; i++) {
+                            const uint32_t poff = (mi * 32 + 4 * (p0 + i) + rr) * 256 + cc * 8;
+                            const uint32_t bo =
+                                (uint32_t)((pld - a.sk_part) + pc * QW_SPLIT_PART + poff) * 4;
+                            const floatx4 q0 = __builtin_bit_cast(
+                                floatx4, __builtin_amdgcn_raw_buffer_load_b128(part_rsrc, bo, 0,
+                                                                               QW_CPOL_COHERENT));
+                            const floatx4 q1 = __builtin_bit_cast(
+                                floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             part_rsrc, bo + 16, 0, QW_CPOL_COHERENT));
+#pragma unroll
+                            for (int j = 0; j < 4; j++) y[i][j] += q0[j], y[i][4 + j] += q1[j];
+                        }
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < RP; i++) lds_row(4 * (p0 + i) + rr, y[i]);
+            }
+            if constexpr (MODE == 1) { /* piece of a split tile: keep the fp32 sums */
+#pragma unroll
+                for (int i = 0; i < RP; i++) {
+                    const uint32_t poff = (mi * 32 + 4 * (p0 + i) + rr) * 256 + cc * 8;
+                    const uint32_t bo = (uint32_t)((pst - a.sk_part) + poff) * 4;
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4, floatx4{y[i][0], y[i][1], y[i][2], y[i][3]}),
+                        part_rsrc, bo, 0, QW_CPOL_COHERENT);
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4, floatx4{y[i][4], y[i][5], y[i][6], y[i][7]}),
+                        part_rsrc, bo + 16, 0, QW_CPOL_COHERENT);
+                }
                 continue;
             }
-            if (pld) { /* all pieces of a split tile, summed in piece order */
-                float t[8];
 #pragma unroll
-                for (int j = 0; j < 8; j++) t[j] = 0.0f;
-                for (uint32_t pc = 0; pc < npart; pc++) {
-                    floatx4 p0, p1;
-                    if (pc == own) {
-                        p0 = floatx4{y[0], y[1], y[2], y[3]};
-                        p1 = floatx4{y[4], y[5], y[6], y[7]};
-                    } else {
-                        const uint32_t bo =
-                            (uint32_t)((pld - a.sk_part) + pc * QW_SPLIT_PART + poff) * 4;
-                        p0 = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             part_rsrc, bo, 0, QW_CPOL_COHERENT));
-                        p1 = __builtin_bit_cast(floatx4,
-                                                __builtin_amdgcn_raw_buffer_load_b128(
-                                                    part_rsrc, bo + 16, 0, QW_CPOL_COHERENT));
-                    }
+            for (int i = 0; i < RP; i++)
 #pragma unroll
-                    for (int j = 0; j < 4; j++) t[j] += p0[j], t[4 + j] += p1[j];
+                for (int j = 0; j < 8; j++) {
+                    float t = y[i][j];
+                    if (scaled) t *= sc[j];
+                    y[i][j] = bf2f(f2bf(t + bias[j]));
                 }
-#pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = t[j];
-            }
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                float t = y[j];
-                if (scaled) t *= sc[j];
-                y[j] = bf2f(f2bf(t + bias[j]));
-            }
-            u16 *dst = a.out + (size_t)row * a.ldc + col;
             if (EPI == QW_EPI_QKNORM && qk_head) {
-                /* the 16 lanes of this row hold one head, 8 elements each
+                /* the 16 lanes of a row hold one head, 8 elements each
                  * (lane cc: elements 8 cc..8 cc + 7), as qw_qk_norm_rope_bf16
                  * holds it: the same sum order, shuffles and roundings */
-                float ss = 0.0f;
+                float ss[RP];
 #pragma unroll
-                for (int j = 0; j < 8; j++) ss = fmaf(y[j], y[j], ss);
+                for (int i = 0; i < RP; i++) {
+                    ss[i] = 0.0f;
 #pragma unroll
-                for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-                const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+                    for (int j = 0; j < 8; j++) ss[i] = fmaf(y[i][j], y[i][j], ss[i]);
+                }
 #pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = bf2f(f2bf(y[j] * inv * nw[j]));
-                const size_t t = (size_t)(row % a.rope_rows) * 64 + 4 * cc;
-                const floatx4 rc = *(const floatx4 *)(a.rope_cos + t);
-                const floatx4 rs = *(const floatx4 *)(a.rope_sin + t);
+                for (int o = 8; o > 0; o >>= 1)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float y0 = y[2 * i] * rc[i] - y[2 * i + 1] * rs[i];
-                    const float y1 = y[2 * i] * rs[i] + y[2 * i + 1] * rc[i];
-                    y[2 * i] = y0;
-                    y[2 * i + 1] = y1;
+                    for (int i = 0; i < RP; i++) ss[i] += __shfl_xor(ss[i], o, 64);
+#pragma unroll
+                for (int i = 0; i < RP; i++) {
+                    const float inv = 1.0f / sqrtf(ss[i] / 128.0f + a.eps);
+#pragma unroll
+                    for (int j = 0; j < 8; j++) y[i][j] = bf2f(f2bf(y[i][j] * inv * nw[j]));
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const float y0 = y[i][2 * q] * rc[i][q] - y[i][2 * q + 1] * rs[i][q];
+                        const float y1 = y[i][2 * q] * rs[i][q] + y[i][2 * q + 1] * rc[i][q];
+                        y[i][2 * q] = y0;
+                        y[i][2 * q + 1] = y1;
+                    }
                 }
             }
-            if (EPI == QW_EPI_GELU) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = gelu_tanh_f(y[j]);
-            } else if (EPI == QW_EPI_GATE) {
-                const u32x4 gv =
-                    *(const u32x4 *)(a.gate + (size_t)a.row_map[row] * a.gate_row_stride + col);
-                const u32x4 rv = *(const u32x4 *)dst;
+            for (int i = 0; i < RP; i++) {
+                if (EPI == QW_EPI_GELU) {
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    y[2 * j] = lo_bf(rv[j]) + y[2 * j] * lo_bf(gv[j]);
-                    y[2 * j + 1] = hi_bf(rv[j]) + y[2 * j + 1] * hi_bf(gv[j]);
+                    for (int j = 0; j < 8; j++) y[i][j] = gelu_tanh_f(y[i][j]);
+                } else if (EPI == QW_EPI_GATE) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        y[i][2 * j] = lo_bf(rv[i][j]) + y[i][2 * j] * lo_bf(gv[i][j]);
+                        y[i][2 * j + 1] = hi_bf(rv[i][j]) + y[i][2 * j + 1] * hi_bf(gv[i][j]);
+                    }
                 }
+                /* non-temporal store (cache policy NT): measured 3% faster
+                 * on the up projection and 8% on 8192^3 than a
+                 * default-policy store */
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    u32x4{pack_bf(y[i][0], y[i][1]), pack_bf(y[i][2], y[i][3]),
+                          pack_bf(y[i][4], y[i][5]), pack_bf(y[i][6], y[i][7])},
+                    out_rsrc, ooff[i], 0, QW_CPOL_NT);
             }
-            /* non-temporal store: measured 3% faster on the up projection
-             * and 8% on 8192^3 than a default-policy store */
-            __builtin_nontemporal_store(u32x4{pack_bf(y[0], y[1]), pack_bf(y[2], y[3]),
-                                              pack_bf(y[4], y[5]), pack_bf(y[6], y[7])},
-                                        (u32x4 *)dst);
         }
     }
+}
+
+template <int EPI, int INT8, int MI, int NI, int RP, class SlabWriter>
+__device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, SlabWriter write_slab,
+                                                  float *region, uint32_t row0, uint32_t col0,
+                                                  uint32_t lane, float *pst, const float *pld,
+                                                  uint32_t npart, uint32_t own) {
+    if (pst)
+        gemm_epilogue_mode<EPI, INT8, MI, NI, RP, 1>(a, write_slab, region, row0, col0, lane, pst,
+                                                     pld, npart, own);
+    else if (pld)
+        gemm_epilogue_mode<EPI, INT8, MI, NI, RP, 2>(a, write_slab, region, row0, col0, lane, pst,
+                                                     pld, npart, own);
+    else
+        gemm_epilogue_mode<EPI, INT8, MI, NI, RP, 0>(a, write_slab, region, row0, col0, lane, pst,
+                                                     pld, npart, own);
 }
 
 template <int WM, int WN, int MI, int NI>
@@ -491,130 +571,10 @@ __device__ __forceinline__ void gemm_pipe_slice(const PipeCtx<A_DL, W_DL, WLD> &
         }
 }
 
-/* Instructions of one kind placed after MFMA i of n: one each after the
- * first `count` MFMAs, or spread evenly (always when there are more than
- * MFMAs, or when `spread`) */
-__device__ constexpr int sched_share(int count, int n, int i, bool spread = false) {
-    return count <= n && !spread ? (i < count ? 1 : 0) : count * (i + 1) / n - count * i / n;
-}
-
-/* 16 x 16 block q (0..3) of a 32 x 32 accumulator's registers (elements
- * 4q..4q+3): the 16x16x32 MFMA path keeps the same accumulator arrays. */
-__device__ __forceinline__ void mfma16_into(floatx16 &acc, int q, bf16x8 a, bf16x8 b) {
-    floatx4 c4 = {acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
-    c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c4, 0, 0, 0);
-    acc[4 * q] = c4[0];
-    acc[4 * q + 1] = c4[1];
-    acc[4 * q + 2] = c4[2];
-    acc[4 * q + 3] = c4[3];
-}
-
-/* gemm_pipe_slice with v_mfma_f32_16x16x32_bf16: two sub-steps of 32 k,
- * 16-row fragments (lane l: row l % 16, k chunk 4 ks + l / 16), block
- * (nb, mb) of C^T in quarter 2 (nb % 2) + mb % 2 of acc[nb / 2][mb / 2];
- * the second sub-step is held back to the start of the next slice (PREV). */
-template <int INT8, int MI, int NI, int A_BYTES, int A_DL, int W_DL, int WLD, int WROWS,
-          bool PREV, bool SPREAD = false>
-__device__ __forceinline__ void gemm_pipe_slice16(const PipeCtx<A_DL, W_DL, WLD> &c,
-                                                  floatx16 (&acc)[NI][MI], bf16x8 (&pa)[2 * MI],
-                                                  bf16x8 (&pw)[2 * NI],
-                                                  const unsigned char *__restrict__ cur,
-                                                  unsigned char *__restrict__ nxt,
-                                                  uint32_t k_next) {
-    typedef __attribute__((address_space(3))) void lds_void;
-    constexpr int MB = 2 * MI, NB = 2 * NI;
-    /* direct loads from inline assembly (see QW_SLICE_END). Measured
-     * against the compiler builtin with its waits: down projection 593 ->
-     * 573 us, the other shapes unchanged. */
-    {
-        const uint32_t nb = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)nxt;
-#pragma unroll
-        for (int j = 0; j < A_DL; j++)
-            gemm_dma16(c.a_rs4, nb + c.a_dst0 + j * 1024, c.a_dvoff[j], k_next * 2);
-#pragma unroll
-        for (int j = 0; j < W_DL; j++)
-            gemm_dma16(c.w_rs4, nb + A_BYTES + c.w_dst0 + j * 1024, c.w_dvoff[j], k_next * 2);
-    }
-    u32x4 rw[WLD];
-    if (INT8) {
-#pragma unroll
-        for (int j = 0; j < WLD; j++)
-            rw[j] = __builtin_bit_cast(
-                u32x4, __builtin_amdgcn_raw_buffer_load_b128(c.w_rsrc, c.w_off[j], k_next, 0));
-    }
-    const unsigned char *As = cur, *Ws = cur + A_BYTES;
-#define QW_FR16(row, ks) ((row) * 128u + (((4 * (ks) + c.h) ^ c.swz) << 4))
-    bf16x8 af[MB], bw[NB], af1[MB], bw1[NB];
-#pragma unroll
-    for (int i = 0; i < MB; i++) af[i] = *(const bf16x8 *)(As + QW_FR16(c.a_row0 + 16 * i, 0));
-#pragma unroll
-    for (int i = 0; i < NB; i++) bw[i] = *(const bf16x8 *)(Ws + QW_FR16(c.w_row0 + 16 * i, 0));
-    if (PREV) {
-#pragma unroll
-        for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-            for (int mb = 0; mb < MB; mb++)
-                mfma16_into(acc[nb >> 1][mb >> 1], 2 * (nb & 1) + (mb & 1), pw[nb], pa[mb]);
-    }
-#pragma unroll
-    for (int i = 0; i < MB; i++) af1[i] = *(const bf16x8 *)(As + QW_FR16(c.a_row0 + 16 * i, 1));
-#pragma unroll
-    for (int i = 0; i < NB; i++) bw1[i] = *(const bf16x8 *)(Ws + QW_FR16(c.w_row0 + 16 * i, 1));
-#undef QW_FR16
-#pragma unroll
-    for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-        for (int mb = 0; mb < MB; mb++)
-            mfma16_into(acc[nb >> 1][mb >> 1], 2 * (nb & 1) + (mb & 1), bw[nb], af[mb]);
-#pragma unroll
-    for (int i = 0; i < MB; i++) pa[i] = af1[i];
-#pragma unroll
-    for (int i = 0; i < NB; i++) pw[i] = bw1[i];
-    if (INT8) {
-        unsigned char *Wn = nxt + A_BYTES;
-#pragma unroll
-        for (int j = 0; j < WLD; j++) {
-            u32x4 lo, hi;
-            i8x16_to_bf16(rw[j], lo, hi);
-            const uint32_t r = c.wr + WROWS * j;
-            *(u32x4 *)(Wn + g_swz(r, 2 * c.wc)) = lo;
-            *(u32x4 *)(Wn + g_swz(r, 2 * c.wc + 1)) = hi;
-        }
-    }
-    constexpr int NMF = MB * NB, NRD = MB + NB;
-    constexpr int NV = A_DL + W_DL + (INT8 ? WLD : 0);
-    constexpr int NW = INT8 ? 2 * WLD : 0;
-    if (PREV) {
-#pragma unroll
-        for (int i = 0; i < NMF; i++) { /* held-back MFMAs: slice loads + fragments of step 0 */
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-#pragma unroll
-            for (int q = 0; q < sched_share(NV, NMF, i); q++)
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-#pragma unroll
-            for (int q = 0; q < sched_share(NRD, NMF, i, SPREAD); q++)
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-    } else {
-        __builtin_amdgcn_sched_group_barrier(0x020, NV, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < NMF; i++) { /* step 0: fragments of step 1, int8 W writes */
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-#pragma unroll
-        for (int q = 0; q < sched_share(NRD, NMF, i, SPREAD); q++)
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-#pragma unroll
-        for (int q = 0; q < sched_share(NW, NMF, i); q++)
-            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
-    }
-}
-
 /* Sums of tile (tm, tn) over k-steps [kb, ke) (64 k each) into acc; the
  * Ends with the LDS
  * stages free (after a barrier). */
-template <int INT8, int WM, int WN, int MI, int NI, int MF = 32, bool SPREAD = false>
+template <int INT8, int WM, int WN, int MI, int NI>
 __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned char *lds,
                                               unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                               uint32_t kb, uint32_t ke,
@@ -726,10 +686,10 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
         }
 #pragma unroll
         for (int j = 0; j < WLD; j++) c.w_off[j] = w_off[j];
-        c.a_row0 = MF == 16 ? wm * (MI * 32) + (lane & 15) : a_row0;
-        c.w_row0 = MF == 16 ? wn * (NI * 32) + (lane & 15) : w_row0;
-        c.swz = MF == 16 ? ((lane & 15) >> 1) & 7u : swz;
-        c.h = MF == 16 ? lane >> 4 : h;
+        c.a_row0 = a_row0;
+        c.w_row0 = w_row0;
+        c.swz = swz;
+        c.h = h;
         c.a_dst0 = wave * (S::BM / NWAVE) * 128;
         c.w_dst0 = wave * (S::BN / NWAVE) * 128;
         c.wr = wr;
@@ -756,36 +716,7 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
         }
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): direct loads landed */
         __syncthreads();
-        if constexpr (MF == 16) {
-            bf16x8 pa[2 * MI], pw[2 * NI]; /* last sub-step's fragments, multiplied one slice late */
-            {
-                const uint32_t nk = (kb + 1 < KT ? kb + 1 : kb) * GBK;
-                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, false, SPREAD>(
-                    c, acc, pa, pw, lds, lds_b, nk);
-                QW_SLICE_END();
-            }
-            /* two slices per trip, so each one's stages are fixed at compile
-             * time and their LDS bases fold into the instructions' offsets */
-            uint32_t kt = kb + 1;
-            for (; kt + 1 < KT; kt += 2) {
-                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true, SPREAD>(
-                    c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
-                QW_SLICE_END();
-                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true, SPREAD>(
-                    c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
-                QW_SLICE_END();
-            }
-            if (kt < KT) { /* the last slice, from stage lds_b */
-                gemm_pipe_slice16<INT8, MI, NI, S::A_BYTES, A_DL, W_DL, WLD, WROWS, true, SPREAD>(
-                    c, acc, pa, pw, lds_b, lds, kt * GBK);
-                QW_SLICE_END();
-            }
-    #pragma unroll
-            for (int nb = 0; nb < 2 * NI; nb++)
-    #pragma unroll
-                for (int mb = 0; mb < 2 * MI; mb++)
-                    mfma16_into(acc[nb >> 1][mb >> 1], 2 * (nb & 1) + (mb & 1), pw[nb], pa[mb]);
-        } else {
+        {
             bf16x8 pa[MI], pw[NI]; /* last sub-step's fragments, multiplied one slice late */
             {
                 const uint32_t nk = (kb + 1 < KT ? kb + 1 : kb) * GBK;
@@ -827,7 +758,7 @@ __device__ __forceinline__ void gemm_mainloop(const qw_gemm_args &a, unsigned ch
 /* Epilogue of a finished tile (bf16 output plus the EPI op), or with pst the
  * fp32 sums of one piece of a split tile, or with pld the sum of all its
  * pieces followed by the epilogue */
-template <int EPI, int INT8, int WM, int WN, int MI, int NI, int MF = 32>
+template <int EPI, int INT8, int WM, int WN, int MI, int NI>
 __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char *lds,
                                             unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                             floatx16 (&acc)[NI][MI], float *pst = nullptr,
@@ -851,20 +782,7 @@ __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char
         const uint32_t poff = wm * (MI * 32) * 256 + wn * (NI * 32);
         constexpr uint32_t LDF = NI * 32 + 4; /* floats per staged row */
         auto write_slab = [&](int mi) __attribute__((always_inline)) {
-            if constexpr (MF == 16) { /* quarter 2p + q: rows 16 q + l % 16, cols 16 p + 4 (l / 16) */
-#pragma unroll
-                for (int ni = 0; ni < NI; ni++)
-#pragma unroll
-                    for (int p = 0; p < 2; p++)
-#pragma unroll
-                        for (int q = 0; q < 2; q++) {
-                            const int k = 2 * p + q;
-                            *(floatx4 *)(region + (16 * q + (lane & 15)) * LDF + ni * 32 + 16 * p +
-                                         4 * (lane >> 4)) =
-                                floatx4{acc[ni][mi][4 * k], acc[ni][mi][4 * k + 1],
-                                        acc[ni][mi][4 * k + 2], acc[ni][mi][4 * k + 3]};
-                        }
-            } else {
+            {
 #pragma unroll
                 for (int ni = 0; ni < NI; ni++)
 #pragma unroll
@@ -874,13 +792,13 @@ __device__ __forceinline__ void gemm_finish(const qw_gemm_args &a, unsigned char
                                     acc[ni][mi][4 * g + 2], acc[ni][mi][4 * g + 3]};
             }
         };
-        gemm_epilogue_lds<EPI, INT8, MI, NI>(a, write_slab, region, row0, col0, lane,
+        gemm_epilogue_lds<EPI, INT8, MI, NI, QW_EPI_RP_D>(a, write_slab, region, row0, col0, lane,
                                              pst ? pst + poff : nullptr, pld ? pld + poff : nullptr,
                                              npart, own);
     }
 }
 
-template <int EPI, int INT8, int WM, int WN, int MI, int NI, int MF = 32, bool SPREAD = false>
+template <int EPI, int INT8, int WM, int WN, int MI, int NI>
 __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned char *lds,
                                              unsigned char *lds_b) {
     const uint32_t KT = a.k / GBK;
@@ -890,27 +808,10 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     floatx16 acc[NI][MI]; /* C^T blocks */
     uint32_t pid = blockIdx.x, tm, tn;
     if (pid < ndp) { /* whole tile; ids XCD-remapped over the whole-tile range */
-        if (MF == 16 && !split) {
-            /* a grid smaller than the tile count walks the tiles in strides
-             * of the grid (the host launches one workgroup per CU); each
-             * tile's epilogue stores drain under the next tile's first
-             * loads. The XCD of id and of id + grid agree (grid % 8 == 0). */
-            for (uint32_t id = pid; id < ndp; id += gridDim.x) {
-                uint32_t q = id;
-                if ((ndp & 7u) == 0) q = (q & 7u) * (ndp >> 3) + (q >> 3);
-                gemm_tile_at(a, q, tm, tn);
-                gemm_mainloop<INT8, WM, WN, MI, NI, MF, SPREAD>(a, lds, lds_b, tm, tn, 0, KT, acc);
-                gemm_finish<EPI, INT8, WM, WN, MI, NI, MF>(a, lds, lds_b, tm, tn, acc);
-                /* every wave's slab reads done before the next tile's loads
-                 * land in the stages (stores may stay in flight) */
-                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-            }
-            return;
-        }
         if ((ndp & 7u) == 0) pid = (pid & 7u) * (ndp >> 3) + (pid >> 3);
         gemm_tile_at(a, pid, tm, tn);
-        gemm_mainloop<INT8, WM, WN, MI, NI, MF, SPREAD>(a, lds, lds_b, tm, tn, 0, KT, acc);
-        gemm_finish<EPI, INT8, WM, WN, MI, NI, MF>(a, lds, lds_b, tm, tn, acc);
+        gemm_mainloop<INT8, WM, WN, MI, NI>(a, lds, lds_b, tm, tn, 0, KT, acc);
+        gemm_finish<EPI, INT8, WM, WN, MI, NI>(a, lds, lds_b, tm, tn, acc);
         return;
     }
     /* Piece of a split tile. Pieces are numbered k-range-major, so the
@@ -923,9 +824,9 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     const uint32_t piece = q / R, r = q % R;
     const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
     gemm_tile_at(a, ndp + r, tm, tn);
-    gemm_mainloop<INT8, WM, WN, MI, NI, MF, SPREAD>(a, lds, lds_b, tm, tn, kb, ke, acc);
+    gemm_mainloop<INT8, WM, WN, MI, NI>(a, lds, lds_b, tm, tn, kb, ke, acc);
     float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
-    gemm_finish<EPI, INT8, WM, WN, MI, NI, MF>(a, lds, lds_b, tm, tn, acc,
+    gemm_finish<EPI, INT8, WM, WN, MI, NI>(a, lds, lds_b, tm, tn, acc,
                                                slots + (size_t)piece * QW_SPLIT_PART);
     /* publish the partial (its coherent stores complete before the
      * workgroup's barrier), then count it. Agent-scope release/acquire
@@ -941,7 +842,7 @@ __device__ __forceinline__ void qw_gemm_impl(const qw_gemm_args &a, unsigned cha
     if (ticket != S - 1) return;
     /* last piece in: the others' partials are read with coherent loads */
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    gemm_finish<EPI, INT8, WM, WN, MI, NI, MF>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S,
+    gemm_finish<EPI, INT8, WM, WN, MI, NI>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S,
                                                piece);
     if (threadIdx.x == 0)
         __hip_atomic_store(a.sk_flag + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -956,24 +857,19 @@ struct GemmLds {
     static constexpr int BYTES = STAGE > SLABS ? STAGE : SLABS;
 };
 
-#define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI, MF, SPREAD)                           \
+#define QW_GEMM_ENTRY(name, EPI, INT8, WM, WN, MI, NI)                           \
     QW_KERNEL void __launch_bounds__(64 * WM * WN, 1) name(qw_gemm_args a) {                 \
         __shared__ __attribute__((aligned(16))) unsigned char lds[GemmLds<WM, WN, MI, NI>::BYTES]; \
         __shared__ __attribute__((aligned(16))) unsigned char lds_b[GemmLds<WM, WN, MI, NI>::BYTES]; \
-        qw_gemm_impl<EPI, INT8, WM, WN, MI, NI, MF, SPREAD>(a, lds, lds_b);                  \
+        qw_gemm_impl<EPI, INT8, WM, WN, MI, NI>(a, lds, lds_b);                  \
     }
 
 /* int8 weights widened in the K loop (linears of fewer than 512 rows, where
- * a separate widening pass would not amortise): 8 waves (two per SIMD) of
- * 64 x 128 with v_mfma_f32_32x32x16_bf16 */
-QW_GEMM_ENTRY(qw_gemm_i8_store_w8, QW_EPI_STORE, 1, 4, 2, 2, 4, 32, false)
-QW_GEMM_ENTRY(qw_gemm_i8_gelu_w8, QW_EPI_GELU, 1, 4, 2, 2, 4, 32, false)
-QW_GEMM_ENTRY(qw_gemm_i8_gate_w8, QW_EPI_GATE, 1, 4, 2, 2, 4, 32, false)
-QW_GEMM_ENTRY(qw_gemm_i8_qkn_w8, QW_EPI_QKNORM, 1, 4, 2, 2, 4, 32, false)
-/* bf16 weights (and int8 weights widened first): the same geometry with
- * each 32 x 32 block computed as four 16 x 16 blocks of
- * v_mfma_f32_16x16x32_bf16 */
-QW_GEMM_ENTRY(qw_gemm_bf16_store_d, QW_EPI_STORE, 0, 4, 2, 2, 4, 16, false)
-QW_GEMM_ENTRY(qw_gemm_bf16_gelu_d, QW_EPI_GELU, 0, 4, 2, 2, 4, 16, true)
-QW_GEMM_ENTRY(qw_gemm_bf16_gate_d, QW_EPI_GATE, 0, 4, 2, 2, 4, 16, true)
-QW_GEMM_ENTRY(qw_gemm_bf16_qkn_d, QW_EPI_QKNORM, 0, 4, 2, 2, 4, 16, false)
+ * a separate widening pass would not amortise, and the allocation-free
+ * entry point): 8 waves (two per SIMD) of 64 x 128 with
+ * v_mfma_f32_32x32x16_bf16. bf16 weights run on the 4-wave kernels of
+ * gemm_q.h. */
+QW_GEMM_ENTRY(qw_gemm_i8_store_w8, QW_EPI_STORE, 1, 4, 2, 2, 4)
+QW_GEMM_ENTRY(qw_gemm_i8_gelu_w8, QW_EPI_GELU, 1, 4, 2, 2, 4)
+QW_GEMM_ENTRY(qw_gemm_i8_gate_w8, QW_EPI_GATE, 1, 4, 2, 2, 4)
+QW_GEMM_ENTRY(qw_gemm_i8_qkn_w8, QW_EPI_QKNORM, 1, 4, 2, 2, 4)

@@ -184,7 +184,7 @@ __device__ __forceinline__ void qg_finish(const qw_gemm_args &a, unsigned char *
                     *(floatx4 *)(region + (16 * q + (lane & 15)) * LDF + ni * 32 + 16 * p +
                                  4 * (lane >> 4)) = acc[2 * mi + q][2 * ni + p];
     };
-    gemm_epilogue_lds<EPI, 0, 4, 4>(a, write_slab, region, row0, col0, lane,
+    gemm_epilogue_lds<EPI, 0, 4, 4, 8>(a, write_slab, region, row0, col0, lane,
                                     pst ? pst + poff : nullptr, pld ? pld + poff : nullptr, npart,
                                     own);
 }

@@ -31,7 +31,7 @@ typedef struct {
     uint32_t lda, ldc;
     uint32_t gate_row_stride; /* elements between modulation rows */
     uint32_t tiles_m, tiles_n;
-    uint32_t a_bytes, w_bytes; /* buffer-resource extents (< 2^31) */
+    uint32_t a_bytes, w_bytes, out_bytes; /* buffer-resource extents (< 2^31) */
     /* Split tiles (split > 1): the first dp_tiles tiles (whole waves of
      * workgroups) run one per workgroup; each remaining tile r is cut into
      * `split` k-ranges, one workgroup each, numbered k-range-major. Every
