@@ -26,8 +26,8 @@ enum {
     K_LN_MOD, K_RMS_ONE, K_QK_NORM_ROPE, K_GATE, K_ACT, K_SWIGLU, K_CAST,
     K_REORDER, K_FILL, K_QUANT, K_DEQUANT, K_COPY2D, K_ATTN,
     /* GEMM kernels in QW_LINEAR_* epilogue order (store, gelu, gate, qknorm) */
-    K_GEMM_I8_STORE_W8, K_GEMM_I8_GELU_W8, K_GEMM_I8_GATE_W8, K_GEMM_I8_QKN_W8,
-    K_GEMM_BF16_STORE_Q, K_GEMM_BF16_GELU_Q, K_GEMM_BF16_GATE_Q, K_GEMM_BF16_QKN_Q, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
+    K_GEMM_BF16_STORE_Q, K_GEMM_BF16_GELU_Q, K_GEMM_BF16_GATE_Q, K_GEMM_BF16_QKN_Q,
+    K_GEMM_I8_STORE_Q, K_GEMM_I8_GELU_Q, K_GEMM_I8_GATE_Q, K_GEMM_I8_QKN_Q, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
     K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_ZERO, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
@@ -35,8 +35,8 @@ static const char *k_names[K_COUNT] = {
     "qw_gate_bf16", "qw_act_bf16", "qw_swiglu_bf16", "qw_cast_f32_bf16",
     "qw_modulation_reorder_bf16", "qw_fill_normal_bf16", "qw_quantize_int8_rows",
     "qw_dequant_int8_f32", "qw_copy2d", "qw_attention_bf16",
-    "qw_gemm_i8_store_w8", "qw_gemm_i8_gelu_w8", "qw_gemm_i8_gate_w8", "qw_gemm_i8_qkn_w8",
     "qw_gemm_bf16_store_q", "qw_gemm_bf16_gelu_q", "qw_gemm_bf16_gate_q", "qw_gemm_bf16_qkn_q",
+    "qw_gemm_i8_store_q", "qw_gemm_i8_gelu_q", "qw_gemm_i8_gate_q", "qw_gemm_i8_qkn_q",
     "qw_widen_i8_bf16",
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16",
     "qw_gemv_bf16_store", "qw_gemv_bf16_gelu", "qw_gemv_i8_store", "qw_gemv_i8_gelu",
@@ -933,7 +933,13 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     /* int8 weights with many rows: widen the weight to bf16 once (exact,
      * unscaled) and run the bf16 GEMM, whose epilogue applies the per-row
      * scale to the fp32 sums -- the same arithmetic as the int8 kernels,
-     * without their in-loop widening. */
+     * without their in-loop widening. At M = 8704 the int8 kernels (int8 W
+     * tiles in LDS, each fragment widened in registers between MFMAs) take
+     * 513-542 / 170-178 / 637-644 / 608-616 us for QKV / out / up / down,
+     * the widening pass plus the bf16 kernel 468-478 / 153-155 / 564-576 /
+     * 591-594 us (same box, alternating): the widening's VALU work does not
+     * hide under the MFMAs. Fewer rows, and the allocation-free entry point,
+     * use the int8 kernels. */
     const int widen = int8 && !no_alloc && d->rows >= QW_WIDEN_MIN_ROWS;
     const void *wptr = d->weight->ptr;
     if (widen) {
@@ -978,14 +984,14 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     /* bf16 weights (or int8 widened above): the 16x16x32-MFMA kernels;
      * int8 weights with few rows: the kernels that widen in their K loop */
     const int qkn = d->epilogue == QW_LINEAR_QKNORM;
-    /* bf16 weights (or int8 widened above): the 4-wave kernels (one wave
-     * per SIMD, 128 x 128 per wave). Same box, alternating, M = 8704, us,
-     * against the 8-wave 16x16x32 kernels they replaced (two waves per
-     * SIMD, 64 x 128 per wave): QKV 447 / 458, out 149 / 155, up (GELU)
-     * 537 / 554, down 598 / 623. */
-    const int useq = !(int8 && !widen);
-    const int kid = (useq ? K_GEMM_BF16_STORE_Q : K_GEMM_I8_STORE_W8) + d->epilogue;
-    const unsigned threads = useq ? 256 : 512, bm = 256, bn = 256;
+    /* the 4-wave kernels (one wave per SIMD, 128 x 128 per wave). Same box,
+     * alternating, M = 8704, us, against the 8-wave 16x16x32 kernels they
+     * replaced (two waves per SIMD, 64 x 128 per wave): QKV 447 / 458, out
+     * 149 / 155, up (GELU) 537 / 554, down 598 / 623; int8 weights in the
+     * loop: 1941-1966 us for the four linears of a layer against 2009-2018
+     * for the 8-wave int8 kernels. */
+    const int kid = (int8 && !widen ? K_GEMM_I8_STORE_Q : K_GEMM_BF16_STORE_Q) + d->epilogue;
+    const unsigned threads = 256, bm = 256, bn = 256;
     a.norm_q = qkn ? (const uint16_t *)d->norm_q->ptr : NULL;
     a.norm_k = qkn ? (const uint16_t *)d->norm_k->ptr : NULL;
     a.rope_cos = qkn ? (const float *)d->rope_cos->ptr : NULL;
@@ -1059,7 +1065,7 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * the tiles, so a tile's output stores drain under the next tile's first
      * loads (up 521 -> 514 us, QKV 365 -> 359 us against one workgroup per
      * tile) */
-    if (useq && a.split == 1 && grid > g->cus && g->cus % 8 == 0)
+    if (a.split == 1 && grid > g->cus && g->cus % 8 == 0)
         grid = g->cus;
     return launch(g, kid, dim3(grid), dim3(threads), a);
 }

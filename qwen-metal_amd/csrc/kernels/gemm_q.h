@@ -1,17 +1,32 @@
-/* bf16 GEMM with one wave per SIMD: a 256 x 256 tile per workgroup of 4
- * waves (2 x 2), each wave a 128 x 128 block of 8 x 8 v_mfma_f32_16x16x32_bf16
- * tiles whose 64 accumulators (256 fp32 per lane) sit in the accumulation
- * registers. Against the 8-wave tile (4 x 2 waves of 64 x 128) it reads a
- * third fewer operand bytes from LDS per MFMA -- each wave's fragments
- * serve 128 rows and 128 columns instead of 64 and 128 -- which is the
- * resource the 8-wave main loop runs out of; each sub-step of 32 k is 64
- * independent MFMAs (1024 matrix-pipe cycles) under which its 16 fragment
- * reads and the next K-slice's 16 direct loads are issued.
+/* The linears' GEMM on CDNA4 matrix cores: out[m, n] = epi(sum_k A[m, k]
+ * W[n, k]), W bf16 or int8 (the "_i8" kernels; per-row scale in the
+ * epilogue), fp32 accumulation, issued as C^T = W A^T (W fragment as the A
+ * operand).
  *
- * Operands, LDS layout, swizzle, direct-to-LDS loads, the held-back
- * sub-step across each K-slice barrier, tile walk, split tiles and the
- * LDS-staged epilogue are those of gemm.h; only the wave geometry and the
- * accumulator arrays differ. out[m, n] = epi(sum_k A[m, k] W[n, k]). */
+ * Geometry: a 256 x 256 tile per workgroup of 4 waves (2 x 2), one wave per
+ * SIMD, each wave a 128 x 128 block of 8 x 8 v_mfma_f32_16x16x32_bf16 tiles
+ * whose 64 accumulators (256 fp32 per lane) sit in the accumulation
+ * registers. Against 8 waves of 64 x 128 it reads a third fewer operand
+ * bytes from LDS per MFMA (each wave's fragments serve 128 rows and 128
+ * columns); each sub-step of 32 k is 64 independent MFMAs (1024
+ * matrix-pipe cycles) under which its 16 fragment reads and the next
+ * K-slice's direct loads are issued.
+ *
+ * Pipeline: K-slices of 64 in two LDS stages (A 256 rows x 128 B, then W),
+ * the next slice's loads in flight while the current one is multiplied. A
+ * and bf16 W go from global memory straight into LDS (buffer_load_dwordx4
+ * ... lds, 1 KB = 8 rows per instruction). 16-byte chunks are XOR-swizzled
+ * by (row / 2) % 8, which a fragment read (16 rows, one chunk) and the
+ * loads' landing slots both respect. Each slice's second sub-step is held
+ * back and multiplied after the slice barrier, under the next slice's
+ * loads and first fragment reads, so the matrix pipe does not drain at the
+ * barrier. (A ring of four 32-k stages, loads three slices ahead, measured
+ * 10-14% slower: twice the barriers and half-line loads.)
+ *
+ * Tiles: one workgroup per CU walks the tiles in strides of the grid
+ * (XCD-consistent), so a tile's output stores drain under the next tile's
+ * loads; a partly filled last wave of tiles can instead be cut into
+ * k-ranges whose fp32 partials meet in memory (split tiles). */
 #pragma once
 #include "gemm.h"
 
@@ -24,6 +39,7 @@ struct QgCtx {
     uint32_t dst0;           /* this wave's 64-row share of a stage */
     uint32_t a_frag, w_frag; /* fragment row base (rows + lane % 16) in bytes */
     uint32_t ch[2];          /* swizzled 16-byte chunk of sub-step 0 / 1 */
+    uint32_t w8[2];          /* int8 W: fragment byte offset of sub-step 0 / 1 */
 };
 
 /* acc += W-fragment x A-fragment, in place. The accumulator is an operand
@@ -52,41 +68,74 @@ __device__ __forceinline__ void qg_read(const QgCtx &c, const unsigned char *cur
  * pa, pw) and runs at the start of the next slice, after the barrier, while
  * that slice's direct loads and first fragments are issued: one direct load
  * and one fragment read every 4 MFMAs; under the 64 MFMAs of sub-step 0 the
- * 16 fragments of sub-step 1 are read, one every 4 MFMAs. */
-template <bool PREV>
+ * 16 fragments of sub-step 1 are read, one every 4 MFMAs.
+ *
+ * int8 W (INT8): the W tile lands in LDS as int8 (256 rows x 64 B, half the
+ * bytes of bf16: 4 direct loads per wave instead of 8); a W fragment is an
+ * 8-byte read, widened to bf16 in registers 16 MFMAs after its read was
+ * issued (its data has landed by then), so the widening's VALU work runs
+ * between MFMAs instead of stalling them. The W fragments are read first in
+ * each sub-step so that all 8 widen before the sub-step ends. */
+template <int INT8, bool PREV>
 __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], bf16x8 (&pa)[8],
                                          bf16x8 (&pw)[8], const unsigned char *__restrict__ cur,
                                          unsigned char *__restrict__ nxt, uint32_t k_next) {
     const uint32_t nl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)nxt;
+    constexpr int NDMA = INT8 ? 12 : 16;
     auto dma = [&](int j) __attribute__((always_inline)) {
         if (j < 8)
             gemm_dma16(c.a_rs4, nl + c.dst0 + j * 1024, c.a_dvoff[j], k_next * 2);
+        else if (INT8)
+            gemm_dma16(c.w_rs4, nl + QG_A_BYTES + c.dst0 / 2 + (j - 8) * 1024, c.w_dvoff[j - 8],
+                       k_next);
         else
             gemm_dma16(c.w_rs4, nl + QG_A_BYTES + c.dst0 + (j - 8) * 1024, c.w_dvoff[j - 8],
                        k_next * 2);
+    };
+    /* fragment j of sub-step ks: bf16 W in consumption order (W block 0, A
+     * blocks 0-7, W blocks 1-7); int8 W blocks 0-7 first, then A blocks 0-7 */
+    auto rd = [&](int ks, int j, bf16x8(&A)[8], bf16x8(&W)[8], u32x2(&RW)[8])
+                  __attribute__((always_inline)) {
+        if (INT8) {
+            if (j < 8)
+                RW[j] = *(const u32x2 *)(cur + QG_A_BYTES + c.w8[ks] + j * 1024);
+            else
+                A[j - 8] = *(const bf16x8 *)(cur + c.a_frag + (j - 8) * 2048 + c.ch[ks]);
+        } else {
+            qg_read(c, cur, c.ch[ks], A, W, j);
+        }
     };
     /* (one direct load and one fragment read every 4 MFMAs measured 7-10%
      * faster than the 16 direct loads issued back to back, than the loads
      * spread over both sub-steps, and than the read placed before the
      * load) */
     bf16x8 af[8], bw[8], af1[8], bw1[8];
+    u32x2 rw[8], rw1[8];
     if (PREV) {
 #pragma unroll
         for (int i = 0; i < 64; i++) {
             QG_MFMA(acc[i & 7][i >> 3], pw[i >> 3], pa[i & 7]);
-            if ((i & 3) == 1) dma(i >> 2);
-            if ((i & 3) == 3) qg_read(c, cur, c.ch[0], af, bw, i >> 2);
+            if ((i & 3) == 1 && (i >> 2) < NDMA) dma(i >> 2);
+            if ((i & 3) == 3) rd(0, i >> 2, af, bw, rw);
+            if (INT8 && (i & 3) == 3 && i >= 19 && ((i - 19) >> 2) < 8)
+                bw[(i - 19) >> 2] = i8x8_to_bf16(rw[(i - 19) >> 2]);
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < 16; j++) dma(j);
+        for (int j = 0; j < NDMA; j++) dma(j);
 #pragma unroll
-        for (int j = 0; j < 16; j++) qg_read(c, cur, c.ch[0], af, bw, j);
+        for (int j = 0; j < 16; j++) rd(0, j, af, bw, rw);
+        if (INT8) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) bw[j] = i8x8_to_bf16(rw[j]);
+        }
     }
 #pragma unroll
     for (int i = 0; i < 64; i++) {
         QG_MFMA(acc[i & 7][i >> 3], bw[i >> 3], af[i & 7]);
-        if ((i & 3) == 3) qg_read(c, cur, c.ch[1], af1, bw1, i >> 2);
+        if ((i & 3) == 3) rd(1, i >> 2, af1, bw1, rw1);
+        if (INT8 && (i & 3) == 3 && i >= 19 && ((i - 19) >> 2) < 8)
+            bw1[(i - 19) >> 2] = i8x8_to_bf16(rw1[(i - 19) >> 2]);
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) pa[i] = af1[i];
@@ -96,6 +145,7 @@ __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
 
 /* Sums of tile (tm, tn) over k-steps [kb, ke) into acc; ends with the LDS
  * stages free (after a barrier). */
+template <int INT8>
 __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char *lds,
                                             unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                             uint32_t kb, uint32_t ke, floatx4 (&acc)[8][8]) {
@@ -109,7 +159,18 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
     for (int j = 0; j < 8; j++) {
         const uint32_t r = wave * 64 + j * 8 + lrow;
         c.a_dvoff[j] = (min(m0 + r, a.m - 1) * a.lda + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
-        c.w_dvoff[j] = (min(n0 + r, a.n - 1) * a.k + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+        if (!INT8)
+            c.w_dvoff[j] = (min(n0 + r, a.n - 1) * a.k + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+    }
+    if (INT8) {
+        /* int8 W rows are 64 B: a direct load covers 16 rows; lane l lands on
+         * row l / 4, physical 16-byte chunk l % 4, which holds logical chunk
+         * (l % 4) ^ ((row / 4) % 4) */
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t r = wave * 64 + j * 16 + (lane >> 2);
+            c.w_dvoff[j] = min(n0 + r, a.n - 1) * a.k + ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
+        }
     }
     c.a_rs4 = gemm_rs4(a.a, a.a_bytes);
     c.w_rs4 = gemm_rs4(a.w, a.w_bytes);
@@ -119,6 +180,10 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
     c.w_frag = (wn * 128 + l16) * 128;
     c.ch[0] = ((0 + h) ^ swz) << 4;
     c.ch[1] = ((4 + h) ^ swz) << 4;
+    /* int8 W fragment: 8-byte chunk 4 ks + lane / 16 of the row, at 8-byte
+     * slot chunk ^ 2 ((row / 4) % 4) (the 16-byte swizzle of the loads) */
+    c.w8[0] = (wn * 128 + l16) * 64 + ((h ^ (2 * ((l16 >> 2) & 3))) << 3);
+    c.w8[1] = (wn * 128 + l16) * 64 + (((4 + h) ^ (2 * ((l16 >> 2) & 3))) << 3);
 #pragma unroll
     for (int mb = 0; mb < 8; mb++)
 #pragma unroll
@@ -130,23 +195,31 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
 #pragma unroll
         for (int j = 0; j < 8; j++)
             gemm_dma16(c.a_rs4, nb + c.dst0 + j * 1024, c.a_dvoff[j], kb * GBK * 2);
+        if (INT8) {
 #pragma unroll
-        for (int j = 0; j < 8; j++)
-            gemm_dma16(c.w_rs4, nb + QG_A_BYTES + c.dst0 + j * 1024, c.w_dvoff[j], kb * GBK * 2);
+            for (int j = 0; j < 4; j++)
+                gemm_dma16(c.w_rs4, nb + QG_A_BYTES + c.dst0 / 2 + j * 1024, c.w_dvoff[j],
+                           kb * GBK);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                gemm_dma16(c.w_rs4, nb + QG_A_BYTES + c.dst0 + j * 1024, c.w_dvoff[j],
+                           kb * GBK * 2);
+        }
     }
     QW_SLICE_END();
     bf16x8 pa[8], pw[8];
-    qg_slice<false>(c, acc, pa, pw, lds, lds_b, (kb + 1 < KT ? kb + 1 : kb) * GBK);
+    qg_slice<INT8, false>(c, acc, pa, pw, lds, lds_b, (kb + 1 < KT ? kb + 1 : kb) * GBK);
     QW_SLICE_END();
     uint32_t kt = kb + 1;
     for (; kt + 1 < KT; kt += 2) {
-        qg_slice<true>(c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
+        qg_slice<INT8, true>(c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
         QW_SLICE_END();
-        qg_slice<true>(c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
+        qg_slice<INT8, true>(c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
         QW_SLICE_END();
     }
     if (kt < KT) {
-        qg_slice<true>(c, acc, pa, pw, lds_b, lds, kt * GBK);
+        qg_slice<INT8, true>(c, acc, pa, pw, lds_b, lds, kt * GBK);
         QW_SLICE_END();
     }
 #pragma unroll
@@ -157,7 +230,7 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 
-template <int EPI>
+template <int EPI, int INT8>
 __device__ __forceinline__ void qg_finish(const qw_gemm_args &a, unsigned char *lds,
                                           unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                           floatx4 (&acc)[8][8], float *pst = nullptr,
@@ -184,12 +257,25 @@ __device__ __forceinline__ void qg_finish(const qw_gemm_args &a, unsigned char *
                     *(floatx4 *)(region + (16 * q + (lane & 15)) * LDF + ni * 32 + 16 * p +
                                  4 * (lane >> 4)) = acc[2 * mi + q][2 * ni + p];
     };
-    gemm_epilogue_lds<EPI, 0, 4, 4, 8>(a, write_slab, region, row0, col0, lane,
-                                    pst ? pst + poff : nullptr, pld ? pld + poff : nullptr, npart,
-                                    own);
+    /* first/second 16-byte halves of the lane's 32 read-back bytes:
+     * lanes 8-15 of a row start with the upper half, so one ds_read_b128
+     * pass covers all 64 banks */
+    const uint32_t cc = lane & 15, swap = (cc >> 3) & 1;
+    auto read_row = [&](uint32_t lr, float (&v)[8]) __attribute__((always_inline)) {
+        const floatx4 v0 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * swap);
+        const floatx4 v1 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * (swap ^ 1));
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[j] = swap ? v1[j] : v0[j];
+            v[4 + j] = swap ? v0[j] : v1[j];
+        }
+    };
+    gemm_epilogue_lds<EPI, INT8, 4, 32, 8>(a, write_slab, read_row, row0, col0, lane,
+                                       pst ? pst + poff : nullptr, pld ? pld + poff : nullptr,
+                                       npart, own);
 }
 
-template <int EPI>
+template <int EPI, int INT8>
 __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *lds,
                                         unsigned char *lds_b) {
     const uint32_t KT = a.k / GBK;
@@ -206,16 +292,16 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
                 uint32_t q = id;
                 if ((ndp & 7u) == 0) q = (q & 7u) * (ndp >> 3) + (q >> 3);
                 gemm_tile_at(a, q, tm, tn);
-                qg_mainloop(a, lds, lds_b, tm, tn, 0, KT, acc);
-                qg_finish<EPI>(a, lds, lds_b, tm, tn, acc);
+                qg_mainloop<INT8>(a, lds, lds_b, tm, tn, 0, KT, acc);
+                qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc);
                 asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             }
             return;
         }
         if ((ndp & 7u) == 0) pid = (pid & 7u) * (ndp >> 3) + (pid >> 3);
         gemm_tile_at(a, pid, tm, tn);
-        qg_mainloop(a, lds, lds_b, tm, tn, 0, KT, acc);
-        qg_finish<EPI>(a, lds, lds_b, tm, tn, acc);
+        qg_mainloop<INT8>(a, lds, lds_b, tm, tn, 0, KT, acc);
+        qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc);
         return;
     }
     /* piece of a split tile (k-range-major numbering, as gemm.h) */
@@ -226,9 +312,9 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
     const uint32_t piece = q / R, r = q % R;
     const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
     gemm_tile_at(a, ndp + r, tm, tn);
-    qg_mainloop(a, lds, lds_b, tm, tn, kb, ke, acc);
+    qg_mainloop<INT8>(a, lds, lds_b, tm, tn, kb, ke, acc);
     float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
-    qg_finish<EPI>(a, lds, lds_b, tm, tn, acc, slots + (size_t)piece * QW_SPLIT_PART);
+    qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc, slots + (size_t)piece * QW_SPLIT_PART);
     __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the partial's stores are done */
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
@@ -238,19 +324,24 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
     __syncthreads();
     if (ticket != S - 1) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    qg_finish<EPI>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S, piece);
+    qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S, piece);
     if (threadIdx.x == 0)
         __hip_atomic_store(a.sk_flag + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-#define QG_ENTRY(name, EPI)                                                                    \
+#define QG_ENTRY(name, EPI, INT8)                                                              \
     QW_KERNEL void __launch_bounds__(256, 1) name(qw_gemm_args a) {                            \
         __shared__ __attribute__((aligned(16))) unsigned char lds[QG_STAGE];                    \
         __shared__ __attribute__((aligned(16))) unsigned char lds_b[QG_STAGE];                  \
-        qg_impl<EPI>(a, lds, lds_b);                                                           \
+        qg_impl<EPI, INT8>(a, lds, lds_b);                                                     \
     }
 
-QG_ENTRY(qw_gemm_bf16_store_q, QW_EPI_STORE)
-QG_ENTRY(qw_gemm_bf16_gelu_q, QW_EPI_GELU)
-QG_ENTRY(qw_gemm_bf16_gate_q, QW_EPI_GATE)
-QG_ENTRY(qw_gemm_bf16_qkn_q, QW_EPI_QKNORM)
+QG_ENTRY(qw_gemm_bf16_store_q, QW_EPI_STORE, 0)
+QG_ENTRY(qw_gemm_bf16_gelu_q, QW_EPI_GELU, 0)
+QG_ENTRY(qw_gemm_bf16_gate_q, QW_EPI_GATE, 0)
+QG_ENTRY(qw_gemm_bf16_qkn_q, QW_EPI_QKNORM, 0)
+/* int8 weights with the per-row scale, widened in registers */
+QG_ENTRY(qw_gemm_i8_store_q, QW_EPI_STORE, 1)
+QG_ENTRY(qw_gemm_i8_gelu_q, QW_EPI_GELU, 1)
+QG_ENTRY(qw_gemm_i8_gate_q, QW_EPI_GATE, 1)
+QG_ENTRY(qw_gemm_i8_qkn_q, QW_EPI_QKNORM, 1)
