@@ -818,11 +818,10 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
  * all of them when there is no full wave), each of its tiles can instead be
  * cut into s k-ranges: R s pieces taking ceil(R s / cus) waves of 1/s the
  * length. s minimises that tail time plus 0.02 (s - 1) for writing and
- * re-reading the fp32 partials, and is used only when that beats half of
- * the whole-tile tail: a split tail costs more than its piece count
- * suggests (M = 8704, K = 12288, N = 3072: 152 tail tiles in 3 pieces
- * 565 us against 530 us for the whole-tile walk; M = 6144, 32 tail tiles
- * in 6 pieces 438 against 494). Pieces stay at least 32 k-steps (2048 k) long: shorter
+ * re-reading the fp32 partials, and is used only when that beats 0.9 of the
+ * whole-tile tail (M = 8704, K = 12288, N = 3072, residual-gate epilogue:
+ * 152 tail tiles in 3 pieces 557-588 us against 573-644 us for the
+ * whole-tile walk, same boxes; 2, 4 or 5 pieces 595-660 us). Pieces stay at least 32 k-steps (2048 k) long: shorter
  * pieces lost more to their partials than they gained (K = 3072 linears
  * measured slower when split, K = 12288 ones faster), and
  * R s <= QW_SPLIT_MAX_PIECES * cus bounds the partial workspace. */
@@ -832,7 +831,7 @@ static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps,
     const uint32_t min_steps = 32;
     const uint32_t G = g->cus, R = tiles % G;
     uint32_t best = 1;
-    double best_t = 0.5;
+    double best_t = 0.9;
     for (uint32_t s = 2; s <= 8; s++) {
         if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * G || (uint64_t)R * s > max_pieces ||
             ksteps < min_steps * s)
