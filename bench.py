@@ -181,7 +181,7 @@ def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, calibrated against
     a copy kernel of known size), or None when it has not been measured."""
-    p = os.path.join(ROOT, "profiles", "gemm_down_bf16_gate_d_traffic.md")
+    p = os.path.join(ROOT, "profiles", "gemm_down_bf16_gate_q_traffic.md")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -456,9 +456,9 @@ def main():
         roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
                     "traffic": measured_traffic(),
-                    "kernel": "qw_gemm_bf16_gate_d (down projection, M=8704 K=12288 N=3072, "
+                    "kernel": "qw_gemm_bf16_gate_q (down projection, M=8704 K=12288 N=3072, "
                               "int8 weight widened by qw_widen_i8_bf16, scale and residual "
-                              "gate in the epilogue)",
+                              "gate in the epilogue, tail tiles split in 3 k-ranges)",
                     "flop_per_launch": fl, "ms_per_launch": down["gemm_ms"],
                     "algorithmic_bytes_per_launch": 2.0 * (down["M"] * down["K"] +
                                                             down["N"] * down["K"] +
