@@ -294,6 +294,34 @@ def profile_attention(qd, gpu, reps=5):
     gpu.submit()
 
 
+def block_320(qd, gpu, reps=10):
+    """BASELINE configs[0] on the GPU: one DiT block (bf16 weights) at 64
+    text + 256 image rows, batch 1, through qw_dit_block, HIP events on the
+    library's stream."""
+    L = qd.lib()
+    H, T, gh, gw = CFG["hidden"], 64, 16, 16
+    R = T + gh * gw
+    cfg = dict(CFG, layers=1, int8_weights=0)
+    dit = qd.Dit(gpu, cfg, SEED)
+    hid = gpu.new(R * H, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, hid.h, 0, hid.n, SEED, 990, 1.0, 0.0), "fill")
+    mod = gpu.new(2 * 6 * H, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, mod.h, 0, mod.n, SEED, 991, 0.2, 0.0), "fill")
+    rm = gpu.put((np.arange(R) < T).astype(np.uint32))
+    cos = np.empty((R, 64), np.float32)
+    sin = np.empty((R, 64), np.float32)
+    L.qw_pipe_rope_tables_host(T, gh, gw, cos.ctypes.data, sin.ctypes.data)
+    ct, st = gpu.put(cos), gpu.put(sin)
+    run = lambda: dit.block(0, hid, mod, ct, st, rm, R, T)  # noqa: E731
+    run()
+    ms = time_ms(gpu, run, reps)
+    F = CFG["mlp_width"]
+    fl = 2.0 * R * (3 * H * H + H * H + 2 * F * H) + 4.0 * 128 * CFG["heads"] * (T * T + (R - T) * R)
+    dit.close()
+    return {"rows": R, "text_rows": T, "ms": ms, "tflops": fl / ms / 1e9,
+            "frac_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS}
+
+
 def denoise_512(qd, gpu):
     """the 32-layer DiT (bf16 weights) in the 8-step
     FlowMatch Euler loop at 512x512 (1024 image + 128 text rows, batch 1,
@@ -464,6 +492,7 @@ def main():
                                                             down["N"] * down["K"] +
                                                             2 * down["M"] * down["N"])}
     sweep = None if args.no_breakdown else sweep_4352(qd, gpu)
+    blk = None if args.no_breakdown else block_320(qd, gpu)
     den = None if args.no_breakdown or args.no_denoise else denoise_512(qd, gpu)
     ti2i = None if args.no_breakdown or args.no_denoise else ti2i_1024(qd, gpu, dit)
     cpu = None if args.no_cpu else cpu_baseline()
@@ -482,6 +511,7 @@ def main():
         "flop_per_step": {"linear": lin, "sdpa": sdpa, "other": extra},
         "breakdown": brk,
         "sweep_4352_bf16": sweep,
+        "block_320_bf16": blk,
         "denoise_512_8step": den,
         "ti2i_1024_one_condition": ti2i,
         "roofline": roofline,
