@@ -41,6 +41,7 @@
 #define ANW QW_ATTN_WAVES           /* waves per workgroup, 32 queries each */
 #define AQB (32 * ANW)              /* queries per workgroup */
 #define A_TILE (AKT * 256)          /* one K or V tile: AKT keys x 128 bf16 */
+static_assert(AQB == QW_ATTN_QROWS, "queries per workgroup");
 
 __device__ __forceinline__ uint32_t attn_limit(const qw_attn_args &a, uint32_t r) {
     if (r >= a.q_rows) return 0;

@@ -170,6 +170,8 @@ typedef struct {
 #ifndef QW_ATTN_WAVES
 #define QW_ATTN_WAVES 8
 #endif
+/* Query rows per attention workgroup (the host sizes the grid with it) */
+#define QW_ATTN_QROWS 256
 
 /* Flash attention over a joint sequence: out[b*q_rows + r] attends keys
  * [b*kv_rows, b*kv_rows + limit(r)) of the same batch entry. */
