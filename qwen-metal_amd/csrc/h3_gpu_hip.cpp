@@ -1064,8 +1064,20 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * the tiles, so a tile's output stores drain under the next tile's first
      * loads (up 521 -> 514 us, QKV 365 -> 359 us against one workgroup per
      * tile) */
-    if (a.split == 1 && grid > g->cus && g->cus % 8 == 0)
+    a.half_from = 0;
+    a.half_count = 0;
+    if (a.split == 1 && grid > g->cus && g->cus % 8 == 0) {
         grid = g->cus;
+        /* a last wave of at most half the CUs' tiles runs as twice as many
+         * half tiles (bf16 W kernels): up projection at M = 8704, 96 tail
+         * tiles of 1632, 577-580 us against 511 us for the 1536 tiles of
+         * M = 8192 */
+        const uint32_t R = tiles % g->cus;
+        if (R && 2 * R <= g->cus && !(int8 && !widen)) {
+            a.half_from = tiles - R;
+            a.half_count = 2 * R;
+        }
+    }
     return launch(g, kid, dim3(grid), dim3(threads), a);
 }
 

@@ -37,6 +37,7 @@ struct QgCtx {
     u32x4 a_rs4, w_rs4;
     uint32_t a_dvoff[8], w_dvoff[8];
     uint32_t dst0;           /* this wave's 64-row share of a stage */
+    uint32_t wdst0;          /* the same for the W tile (half tiles: A has 32 rows per wave) */
     uint32_t a_frag, w_frag; /* fragment row base (rows + lane % 16) in bytes */
     uint32_t ch[2];          /* swizzled 16-byte chunk of sub-step 0 / 1 */
     uint32_t w8[2];          /* int8 W: fragment byte offset of sub-step 0 / 1 */
@@ -230,16 +231,133 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 
-template <int EPI, int INT8>
-__device__ __forceinline__ void qg_finish(const qw_gemm_args &a, unsigned char *lds,
-                                          unsigned char *lds_b, uint32_t tm, uint32_t tn,
-                                          floatx4 (&acc)[8][8], float *pst = nullptr,
-                                          const float *pld = nullptr, uint32_t npart = 0,
-                                          uint32_t own = 0) {
+/* Half tiles (128 x 256, bf16 W): a tile walk whose last wave of tiles
+ * would leave at least half the CUs idle runs those tiles as twice as many
+ * half tiles instead. Same 2 x 2 waves, each 64 x 128 (4 x 8 MFMA tiles);
+ * the A stage holds 128 rows (4 direct loads per wave), the W stage is the
+ * full tile's. Per 32-k sub-step: 32 MFMAs, 12 fragments (W block 0, A
+ * blocks 0-3, W blocks 1-7), and under the held-back sub-step the 12 direct
+ * loads of the next slice, one load and one read every 2 MFMAs. */
+template <bool PREV>
+__device__ __forceinline__ void qh_slice(const QgCtx &c, floatx4 (&acc)[8][8], bf16x8 (&pa)[8],
+                                         bf16x8 (&pw)[8], const unsigned char *__restrict__ cur,
+                                         unsigned char *__restrict__ nxt, uint32_t k_next) {
+    const uint32_t nl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)nxt;
+    auto dma = [&](int j) __attribute__((always_inline)) {
+        if (j < 4)
+            gemm_dma16(c.a_rs4, nl + c.dst0 + j * 1024, c.a_dvoff[j], k_next * 2);
+        else
+            gemm_dma16(c.w_rs4, nl + QG_A_BYTES + c.wdst0 + (j - 4) * 1024, c.w_dvoff[j - 4],
+                       k_next * 2);
+    };
+    auto rd = [&](int ks, int j, bf16x8(&A)[8], bf16x8(&W)[8]) __attribute__((always_inline)) {
+        if (j == 0)
+            W[0] = *(const bf16x8 *)(cur + QG_A_BYTES + c.w_frag + c.ch[ks]);
+        else if (j <= 4)
+            A[j - 1] = *(const bf16x8 *)(cur + c.a_frag + (j - 1) * 2048 + c.ch[ks]);
+        else
+            W[j - 4] = *(const bf16x8 *)(cur + QG_A_BYTES + c.w_frag + (j - 4) * 2048 + c.ch[ks]);
+    };
+    bf16x8 af[8], bw[8], af1[8], bw1[8];
+    if (PREV) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            QG_MFMA(acc[i & 3][i >> 2], pw[i >> 2], pa[i & 3]);
+            if ((i & 1) == 0 && (i >> 1) < 12) dma(i >> 1);
+            if ((i & 1) == 1 && (i >> 1) < 12) rd(0, i >> 1, af, bw);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 12; j++) dma(j);
+#pragma unroll
+        for (int j = 0; j < 12; j++) rd(0, j, af, bw);
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        QG_MFMA(acc[i & 3][i >> 2], bw[i >> 2], af[i & 3]);
+        if ((i & 1) == 1 && (i >> 1) < 12) rd(1, i >> 1, af1, bw1);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) pa[i] = af1[i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) pw[i] = bw1[i];
+}
+
+/* Sums of the half tile at rows [m0, m0 + 128), columns [n0, n0 + 256) over
+ * all of K into acc[0..3][*]; ends with the LDS stages free. */
+__device__ __forceinline__ void qh_mainloop(const qw_gemm_args &a, unsigned char *lds,
+                                            unsigned char *lds_b, uint32_t m0, uint32_t n0,
+                                            floatx4 (&acc)[8][8]) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave >> 1, wn = wave & 1;
-    const uint32_t row0 = tm * 256 + wm * 128, col0 = tn * 256 + wn * 128;
+    QgCtx c;
+    const uint32_t lrow = lane >> 3, lp = lane & 7;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t r = wave * 32 + j * 8 + lrow;
+        c.a_dvoff[j] = (min(m0 + r, a.m - 1) * a.lda + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t r = wave * 64 + j * 8 + lrow;
+        c.w_dvoff[j] = (min(n0 + r, a.n - 1) * a.k + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+    }
+    c.a_rs4 = gemm_rs4(a.a, a.a_bytes);
+    c.w_rs4 = gemm_rs4(a.w, a.w_bytes);
+    c.dst0 = wave * 32 * 128;
+    c.wdst0 = wave * 64 * 128;
+    const uint32_t l16 = lane & 15, h = lane >> 4, swz = (l16 >> 1) & 7u;
+    c.a_frag = (wm * 64 + l16) * 128;
+    c.w_frag = (wn * 128 + l16) * 128;
+    c.ch[0] = ((0 + h) ^ swz) << 4;
+    c.ch[1] = ((4 + h) ^ swz) << 4;
+#pragma unroll
+    for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+        for (int nb = 0; nb < 8; nb++) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t KT = a.k / GBK;
+    {
+        const uint32_t nb =
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)lds;
+#pragma unroll
+        for (int j = 0; j < 4; j++) gemm_dma16(c.a_rs4, nb + c.dst0 + j * 1024, c.a_dvoff[j], 0);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            gemm_dma16(c.w_rs4, nb + QG_A_BYTES + c.wdst0 + j * 1024, c.w_dvoff[j], 0);
+    }
+    QW_SLICE_END();
+    bf16x8 pa[8], pw[8];
+    qh_slice<false>(c, acc, pa, pw, lds, lds_b, (1 < KT ? 1 : 0) * GBK);
+    QW_SLICE_END();
+    uint32_t kt = 1;
+    for (; kt + 1 < KT; kt += 2) {
+        qh_slice<true>(c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
+        QW_SLICE_END();
+        qh_slice<true>(c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
+        QW_SLICE_END();
+    }
+    if (kt < KT) {
+        qh_slice<true>(c, acc, pa, pw, lds_b, lds, kt * GBK);
+        QW_SLICE_END();
+    }
+#pragma unroll
+    for (int i = 0; i < 32; i++) QG_MFMA(acc[i & 3][i >> 2], pw[i >> 2], pa[i & 3]);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
+/* The epilogue of the tile (MB = 8) or half tile (MB = 4) whose rows start
+ * at m0 and columns at n0: each wave's MB x 8 accumulator blocks. */
+template <int EPI, int INT8, int MB>
+__device__ __forceinline__ void qg_finish_at(const qw_gemm_args &a, unsigned char *lds,
+                                             unsigned char *lds_b, uint32_t m0, uint32_t n0,
+                                             floatx4 (&acc)[8][8], float *pst = nullptr,
+                                             const float *pld = nullptr, uint32_t npart = 0,
+                                             uint32_t own = 0) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    const uint32_t row0 = m0 + wm * (MB * 16), col0 = n0 + wn * 128;
     constexpr uint32_t LDF = 128 + 4, REG = 32 * LDF * 4;
     /* waves 0, 1 stage through `lds`, 2, 3 through `lds_b` (free after the
      * loop's last barrier), one 32-row slab (16.5 KB) at a time */
@@ -270,9 +388,18 @@ __device__ __forceinline__ void qg_finish(const qw_gemm_args &a, unsigned char *
             v[4 + j] = swap ? v0[j] : v1[j];
         }
     };
-    gemm_epilogue_lds<EPI, INT8, 4, 32, 8>(a, write_slab, read_row, row0, col0, lane,
-                                       pst ? pst + poff : nullptr, pld ? pld + poff : nullptr,
-                                       npart, own);
+    gemm_epilogue_lds<EPI, INT8, MB / 2, 32, 8>(a, write_slab, read_row, row0, col0, lane,
+                                            pst ? pst + poff : nullptr,
+                                            pld ? pld + poff : nullptr, npart, own);
+}
+
+template <int EPI, int INT8>
+__device__ __forceinline__ void qg_finish(const qw_gemm_args &a, unsigned char *lds,
+                                          unsigned char *lds_b, uint32_t tm, uint32_t tn,
+                                          floatx4 (&acc)[8][8], float *pst = nullptr,
+                                          const float *pld = nullptr, uint32_t npart = 0,
+                                          uint32_t own = 0) {
+    qg_finish_at<EPI, INT8, 8>(a, lds, lds_b, tm * 256, tn * 256, acc, pst, pld, npart, own);
 }
 
 template <int EPI, int INT8>
@@ -287,13 +414,26 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
     if (pid < ndp) {
         if (!split) {
             /* one workgroup per CU walks the tiles in strides of the grid;
-             * id and id + grid sit on the same XCD (grid % 8 == 0) */
-            for (uint32_t id = pid; id < ndp; id += gridDim.x) {
-                uint32_t q = id;
-                if ((ndp & 7u) == 0) q = (q & 7u) * (ndp >> 3) + (q >> 3);
-                gemm_tile_at(a, q, tm, tn);
-                qg_mainloop<INT8>(a, lds, lds_b, tm, tn, 0, KT, acc);
-                qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc);
+             * id and id + grid sit on the same XCD (grid % 8 == 0). Tiles
+             * [half_from, nt) run as half tiles, ids half_from + [0, 2 R):
+             * the two halves of a tile go to one XCD. */
+            const uint32_t H = INT8 ? 0u : a.half_count;
+            const uint32_t F = H ? a.half_from : ndp;
+            for (uint32_t id = pid; id < F + H; id += gridDim.x) {
+                if (id < F) {
+                    uint32_t q = id;
+                    if ((F & 7u) == 0) q = (q & 7u) * (F >> 3) + (q >> 3);
+                    gemm_tile_at(a, q, tm, tn);
+                    qg_mainloop<INT8>(a, lds, lds_b, tm, tn, 0, KT, acc);
+                    qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc);
+                } else if (!INT8) {
+                    uint32_t hq = id - F;
+                    if ((H & 15u) == 0) hq = (hq & 7u) * (H >> 3) + (hq >> 3);
+                    gemm_tile_at(a, F + (hq >> 1), tm, tn);
+                    const uint32_t m0 = tm * 256 + (hq & 1) * 128;
+                    qh_mainloop(a, lds, lds_b, m0, tn * 256, acc);
+                    qg_finish_at<EPI, INT8, 4>(a, lds, lds_b, m0, tn * 256, acc);
+                }
                 asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
             }
             return;

@@ -47,6 +47,9 @@ typedef struct {
     const float *rope_cos, *rope_sin;
     uint32_t rope_rows, qk_cols;
     float eps;
+    /* Tile walk (split <= 1, bf16 W): tiles [half_from, tiles) run as
+     * half_count = 2 (tiles - half_from) half tiles of 128 x 256; 0: none */
+    uint32_t half_from, half_count;
 } qw_gemm_args;
 
 typedef struct {

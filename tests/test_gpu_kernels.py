@@ -236,23 +236,35 @@ def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
     assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
-@pytest.mark.parametrize("epi", ["store", "gelu"])
+@pytest.mark.parametrize("epi", ["store", "gelu", "gate"])
 def test_linear_tile_walk(gpu, qd, oracle, epi):
     """More tiles than compute units: the 16x16x32 GEMM launches one
     workgroup per CU and each walks its tiles in strides of the grid. 17 x
     17 tiles of 256 x 256 (289 > 256), ragged in both the last tile row
     (4100 rows) and the last tile column (4104 columns), called twice in a
-    row (the workgroups keep no state between tiles or calls)."""
+    row (the workgroups keep no state between tiles or calls). The 33 tiles
+    of the last, partly filled wave run as 66 half tiles of 128 x 256; the
+    last tile row's second halves hold no rows at all."""
     rows, k, n = 4100, 256, 4104
     x = synth(oracle, rows * k, 41)
     w = synth(oracle, n * k, 42, 0.02)
     b = synth(oracle, n, 43, 0.02)
     xt, wt, bt = gpu.put(x), gpu.put(w), gpu.put(b)
+    slots = 6
+    mod = synth(oracle, 2 * slots * n, 44, 0.5)
+    rm = (np.arange(rows) % 3 == 0).astype(np.uint32)
+    h0 = synth(oracle, rows * n, 45)
+    mt, rmt = gpu.put(mod), gpu.put(rm)
     outs = []
     for _ in range(2):
-        out = gpu.new(rows * n, qd.BF16)
-        gpu.linear(out, xt, wt, rows, k, n, bias=bt,
-                   epilogue=qd.LINEAR_GELU if epi == "gelu" else qd.LINEAR_STORE)
+        if epi == "gate":
+            out = gpu.put(h0)
+            gpu.linear(out, xt, wt, rows, k, n, bias=bt, epilogue=qd.LINEAR_GATE,
+                       modulation=mt, row_map=rmt, slots=slots, gate_slot=2)
+        else:
+            out = gpu.new(rows * n, qd.BF16)
+            gpu.linear(out, xt, wt, rows, k, n, bias=bt,
+                       epilogue=qd.LINEAR_GELU if epi == "gelu" else qd.LINEAR_STORE)
         gpu.submit()
         outs.append(out.read())
     assert np.array_equal(outs[0], outs[1])
@@ -263,15 +275,34 @@ def test_linear_tile_walk(gpu, qd, oracle, epi):
         assert_linear_close(oracle, outs[0], lin, mag)
         return
     want = np.empty_like(lin)
-    oracle.lib().qo_gelu_tanh(want, lin, lin.size)
+    f = oracle.bf16_to_f32
+    if epi == "gate":
+        want = np.empty(rows * n, np.uint16)
+        oracle.lib().qo_gate(want, h0, lin, mod, rm, rows, n, slots, 2)
+    else:
+        oracle.lib().qo_gelu_tanh(want, lin, lin.size)
     d = ulp_diff(outs[0], want)
-    diff = np.abs(oracle.bf16_to_f32(outs[0]).astype(np.float64) - oracle.bf16_to_f32(want))
+    diff = np.abs(f(outs[0]).astype(np.float64) - f(want))
     ok = (d <= 2) | (diff <= 2.0 ** -13 * mag)
+    if epi == "gate":
+        # where the sum sits at a rounding boundary of y = bf16(sum), y can
+        # round the other way (one bf16 ulp of y); the output then moves by
+        # |g| ulp(y) plus its own rounding, many output ulps where h + y g
+        # cancels
+        g = f(mod).reshape(2, slots, n)[rm, 2, :].ravel().astype(np.float64)
+        down, up = bf16_neighbours(lin)
+        ulp_y = np.maximum(np.abs(f(up) - f(lin)), np.abs(f(lin) - f(down)))
+        wd, wu = bf16_neighbours(want)
+        ulp_o = np.maximum(np.abs(f(wu) - f(want)), np.abs(f(want) - f(wd)))
+        ok |= diff <= np.abs(g) * ulp_y + ulp_o
     assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
 @pytest.mark.parametrize("rows,int8,rope_rows", [(300, False, 300), (300, True, 150),
-                                                 (1000, True, 500), (4357, False, 4357)])
+                                                 (1000, True, 500), (4357, False, 4357),
+                                                 # 270 tiles: a tile walk whose last 14
+                                                 # tiles run as half tiles
+                                                 (11400, False, 11400)])
 def test_linear_qknorm_epilogue_bit_identical(gpu, qd, oracle, rows, int8, rope_rows):
     """The fused q|k|v linear with the per-head RMS norm and RoPE of q and k
     in its epilogue equals the linear followed by qw_gpu_qk_norm_rope_bf16,
