@@ -105,9 +105,11 @@ __device__ __forceinline__ void attn_store_rows(const qw_attn_args &a, const flo
  * M0 = the wave's LDS base, lane l writes base + 16 l. Issued from inline
  * assembly so the compiler does not treat it as a pending LDS store (it
  * would wait for every one in flight before each LDS read); the kernel
- * waits for them itself (vmcnt) before the barrier that publishes a tile. */
+ * waits for them itself (vmcnt) before the barrier that publishes a tile. The
+ * load reads M0 one wait state after its write at the earliest (gfx9 rule;
+ * the compiler does not see inside the asm to insert it). */
 __device__ __forceinline__ void attn_dma(u32x4 rsrc, uint32_t lds_base, uint32_t voff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                  :
                  : "s"(lds_base), "v"(voff), "s"(rsrc)
                  : "m0");

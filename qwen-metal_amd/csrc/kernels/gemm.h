@@ -409,7 +409,9 @@ __device__ __forceinline__ void gemm_epilogue_lds(const qw_gemm_args &a, SlabWri
 /* buffer_load_dwordx4 ... lds from inline assembly: M0 = LDS address,
  * lane l writes M0 + 16 l */
 __device__ __forceinline__ void gemm_dma16(u32x4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+    /* s_nop 0: an LDS-direct load reads M0 at least one wait state after
+     * an SALU write of it (gfx9); inside the asm the compiler cannot add it */
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
                  : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
                  : "m0");

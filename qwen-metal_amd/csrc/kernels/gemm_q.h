@@ -51,6 +51,13 @@ struct QgCtx {
  * MFMAs, the direct loads and the fragment reads issue in source order. */
 #define QG_MFMA(acc, w, x) \
     asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(w), "v"(x))
+/* The first MFMA of an accumulator (srcC = 0) defines it: no zeroing
+ * instruction precedes the MFMAs. An asm MFMA is invisible to the compiler's
+ * hazard tracking, so a VALU write of an accumulator placed right before the
+ * MFMA that reads it (fewer than the 2 wait states gfx9 requires) would feed
+ * it the old value; with no such writes there is nothing to misplace. */
+#define QG_MFMA0(acc, w, x) \
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(w), "v"(x))
 
 /* fragment j of a sub-step, in the order its MFMAs consume them (W block 0,
  * A blocks 0-7, W blocks 1-7) */
@@ -133,7 +140,10 @@ __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
     }
 #pragma unroll
     for (int i = 0; i < 64; i++) {
-        QG_MFMA(acc[i & 7][i >> 3], bw[i >> 3], af[i & 7]);
+        if (PREV)
+            QG_MFMA(acc[i & 7][i >> 3], bw[i >> 3], af[i & 7]);
+        else
+            QG_MFMA0(acc[i & 7][i >> 3], bw[i >> 3], af[i & 7]);
         if ((i & 3) == 3) rd(1, i >> 2, af1, bw1, rw1);
         if (INT8 && (i & 3) == 3 && i >= 19 && ((i - 19) >> 2) < 8)
             bw1[(i - 19) >> 2] = i8x8_to_bf16(rw1[(i - 19) >> 2]);
@@ -185,10 +195,6 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
      * slot chunk ^ 2 ((row / 4) % 4) (the 16-byte swizzle of the loads) */
     c.w8[0] = (wn * 128 + l16) * 64 + ((h ^ (2 * ((l16 >> 2) & 3))) << 3);
     c.w8[1] = (wn * 128 + l16) * 64 + (((4 + h) ^ (2 * ((l16 >> 2) & 3))) << 3);
-#pragma unroll
-    for (int mb = 0; mb < 8; mb++)
-#pragma unroll
-        for (int nb = 0; nb < 8; nb++) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t KT = ke;
     {
         const uint32_t nb =
@@ -274,7 +280,10 @@ __device__ __forceinline__ void qh_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
     }
 #pragma unroll
     for (int i = 0; i < 32; i++) {
-        QG_MFMA(acc[i & 3][i >> 2], bw[i >> 2], af[i & 3]);
+        if (PREV)
+            QG_MFMA(acc[i & 3][i >> 2], bw[i >> 2], af[i & 3]);
+        else
+            QG_MFMA0(acc[i & 3][i >> 2], bw[i >> 2], af[i & 3]);
         if ((i & 1) == 1 && (i >> 1) < 12) rd(1, i >> 1, af1, bw1);
     }
 #pragma unroll
@@ -312,10 +321,6 @@ __device__ __forceinline__ void qh_mainloop(const qw_gemm_args &a, unsigned char
     c.w_frag = (wn * 128 + l16) * 128;
     c.ch[0] = ((0 + h) ^ swz) << 4;
     c.ch[1] = ((4 + h) ^ swz) << 4;
-#pragma unroll
-    for (int mb = 0; mb < 4; mb++)
-#pragma unroll
-        for (int nb = 0; nb < 8; nb++) acc[mb][nb] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t KT = a.k / GBK;
     {
         const uint32_t nb =
@@ -470,11 +475,7 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
 }
 
 /* One LDS array fixes the layout: the first stage at offset 0, the second
- * at 64 KB, the split-tile counter after them. (With the two stages as
- * separate arrays the compiler chose their order; with the first stage
- * placed after the second, the int8-weight kernels' results were wrong
- * while the bf16 kernels' were right -- cause not found -- so the order is
- * not left to it.) */
+ * at 64 KB, the split-tile counter after them. */
 #define QG_ENTRY(name, EPI, INT8)                                                              \
     QW_KERNEL void __launch_bounds__(256, 1) name(qw_gemm_args a) {                            \
         __shared__ __attribute__((aligned(16))) unsigned char smem[2 * QG_STAGE + 16];          \
