@@ -155,6 +155,82 @@ def sweep_4352(qd, gpu, reps=10):
     return res
 
 
+def vendor_gemm(qd, gpu, reps=20):
+    """The step's attention (against torch's SDPA) and the four step linears (bf16 W N(0, 0.02), X N(0, 1), plain store, no
+    bias) through this library's GEMM and through the vendor library's
+    (torch.matmul -> hipBLASLt), alternating, same inputs' distribution:
+    a frame for the roofline fraction, not part of the product path."""
+    import torch
+    H, F, M = CFG["hidden"], CFG["mlp_width"], 2 * (TEXT + GH * GW)
+    L = qd.lib()
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    res = {}
+    for name, k, n in (("qkv", H, 3 * H), ("out", H, H), ("up", H, F), ("down", F, H)):
+        x = gpu.new(M * k, qd.BF16)
+        w = gpu.new(n * k, qd.BF16)
+        out = gpu.new(M * n, qd.BF16)
+        gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, x.h, 0, x.n, 1, 21, 1.0, 0.0), "fill")
+        gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, w.h, 0, w.n, 1, 22, 0.02, 0.0), "fill")
+        run = lambda: gpu.linear(out, x, w, M, k, n)  # noqa: E731
+        run()
+        tx = torch.randn(M, k, device=dev, dtype=torch.bfloat16, generator=gen)
+        tw = (torch.randn(n, k, device=dev, dtype=torch.bfloat16, generator=gen) * 0.02)
+        to = torch.empty(M, n, device=dev, dtype=torch.bfloat16)
+        torch.matmul(tx, tw.t(), out=to)
+        torch.cuda.synchronize()
+        fl = 2.0 * M * n * k
+        ours, vend = [], []
+        for _ in range(3):
+            ours.append(time_ms(gpu, run, reps))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                torch.matmul(tx, tw.t(), out=to)
+            e1.record()
+            torch.cuda.synchronize()
+            vend.append(e0.elapsed_time(e1) / reps)
+        o, v = min(ours), min(vend)
+        res[name] = {"M": M, "K": k, "N": n, "ours_ms": o, "vendor_ms": v,
+                     "ours_tflops": fl / o / 1e9, "vendor_tflops": fl / v / 1e9,
+                     "ours_over_vendor": v / o}
+        for b in (x, w, out):
+            b.free()
+        del tx, tw, to
+    # the step's attention (joint, full, B 2 x 24 heads x 4352 rows, d 128)
+    # against torch's scaled_dot_product_attention on the same shape
+    R = TEXT + GH * GW
+    qkv = gpu.new(M * 3 * H, qd.BF16)
+    att = gpu.new(M * H, qd.BF16)
+    gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, qkv.h, 0, M * 3 * H, 1, 3, 1.0, 0.0), "fill")
+    run = lambda: gpu.attention(att, qkv, qkv, qkv, BATCH, R, R, CFG["heads"], 3 * H,  # noqa
+                                3 * H, 3 * H, H, 0, H, 2 * H, text_rows=TEXT, text_causal=0)
+    run()
+    tq, tk, tv = (torch.randn(BATCH, CFG["heads"], R, H // CFG["heads"], device=dev,
+                              dtype=torch.bfloat16, generator=gen) for _ in range(3))
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    sdpa(tq, tk, tv)
+    torch.cuda.synchronize()
+    ours, vend = [], []
+    for _ in range(3):
+        ours.append(time_ms(gpu, run, 10))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            sdpa(tq, tk, tv)
+        e1.record()
+        torch.cuda.synchronize()
+        vend.append(e0.elapsed_time(e1) / 10)
+    _, sd, _ = flops(dict(CFG, layers=1), R, TEXT, BATCH)
+    o, v = min(ours), min(vend)
+    res["attention"] = {"batch": BATCH, "rows": R, "heads": CFG["heads"], "ours_ms": o,
+                        "vendor_ms": v, "ours_tflops": sd / o / 1e9,
+                        "vendor_tflops": sd / v / 1e9, "ours_over_vendor": v / o}
+    qkv.free()
+    att.free()
+    return res
+
+
 def epilogue_operands(qd, gpu, M, R):
     """Operands of the step's fused epilogues: the modulation (6 slots, gate
     slots 2 / 3 through the row map of the batch-2 stack) and the q/k norm
@@ -428,14 +504,24 @@ def main():
                     choices=["down", "attention"],
                     help="only launch a calibration copy and the dominant GEMM (default) or "
                          "the attention kernel, for rocprofv3 --pmc")
+    ap.add_argument("--vendor", action="store_true",
+                    help="only time the four step linears (bf16 W) here and through "
+                         "torch.matmul (hipBLASLt), alternating, and print that line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
+    if args.vendor:
+        import torch  # its HIP runtime takes the device before this library's
+        torch.zeros(1, device="cuda:0")
     qd = load_qdit()
     gpu = qd.Gpu()
+    if args.vendor:
+        print(json.dumps({"vendor_gemm": vendor_gemm(qd, gpu)}))
+        gpu.close()
+        return
     if args.profile_kernel:
         (profile_attention if args.profile_kernel == "attention" else profile_kernel)(qd, gpu)
         gpu.close()
