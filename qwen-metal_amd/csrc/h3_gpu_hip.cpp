@@ -1198,7 +1198,7 @@ extern "C" int qw_gpu_attention_bf16(h3_gpu *g, const qw_attention_desc *d) {
     g->stats.mps_sdpa_dispatches += 0;
     if (((uint64_t)(d->kv_rows - 1) * std::max(d->ldk, d->ldv) + hd) * 2 >= (1ull << 31))
         return fail(g, "attention: one batch entry's K/V exceed 2 GiB");
-    const uint32_t aqb = QW_ATTN_QROWS;
+    const uint32_t aqb = g->attn_threads / 2; /* 32 query rows per 64-lane wave */
     const uint64_t nwg = (uint64_t)((d->q_rows + aqb - 1) / aqb) * d->heads * d->batch;
     if (nwg >= (1ull << 31)) return fail(g, "attention: grid too large");
     return launch(g, K_ATTN, dim3((uint32_t)nwg), dim3(g->attn_threads), a);

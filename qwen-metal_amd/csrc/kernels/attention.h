@@ -108,10 +108,11 @@ __device__ __forceinline__ void attn_store_rows(const qw_attn_args &a, const flo
  * waits for them itself (vmcnt) before the barrier that publishes a tile. The
  * load reads M0 one wait state after its write at the earliest (gfx9 rule;
  * the compiler does not see inside the asm to insert it). */
-__device__ __forceinline__ void attn_dma(u32x4 rsrc, uint32_t lds_base, uint32_t voff) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+__device__ __forceinline__ void attn_dma(u32x4 rsrc, uint32_t lds_base, uint32_t voff,
+                                         uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
-                 : "s"(lds_base), "v"(voff), "s"(rsrc)
+                 : "s"(lds_base), "v"(voff), "s"(rsrc), "s"(soff)
                  : "m0");
 }
 
@@ -212,18 +213,38 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)lds;
     const uint32_t drow = lane >> 4, dphys = lane & 15;
+    /* lane offsets of the wave's loads relative to the tile's first key row
+     * (whose byte offset kv0 * ld * 2 goes in the scalar offset); rows past
+     * the last key are clamped to it, which only the last tile needs */
+    uint32_t kvo[DPW], vvo[DPW];
+#pragma unroll
+    for (int jj = 0; jj < DPW; jj++) {
+        const uint32_t row = (wave * DPW + jj) * 4 + drow;
+        kvo[jj] = (row * a.ldk + ((dphys ^ (row & 15)) * 8)) * 2;
+        vvo[jj] = (row * a.ldv + ((dphys ^ (4 * (row & 3))) * 8)) * 2;
+    }
     auto issue = [&](uint32_t kstage, uint32_t kv0k, uint32_t vstage, uint32_t kv0v)
         __attribute__((always_inline)) {
+        if (kv0k + AKT <= a.kv_rows) {
+#pragma unroll
+            for (int jj = 0; jj < DPW; jj++) {
+                const uint32_t blk = wave * DPW + jj; /* 1 KB block of the tile */
+                attn_dma(rk, lds0 + kstage * A_TILE + blk * 1024, kvo[jj], kv0k * a.ldk * 2);
+                attn_dma(rv, lds0 + (2 + vstage) * A_TILE + blk * 1024, vvo[jj],
+                         kv0v * a.ldv * 2);
+            }
+            return;
+        }
 #pragma unroll
         for (int jj = 0; jj < DPW; jj++) {
-            const uint32_t blk = wave * DPW + jj;     /* 1 KB block of the tile */
-            const uint32_t row = blk * 4 + drow;      /* key row in the tile */
+            const uint32_t blk = wave * DPW + jj;
+            const uint32_t row = blk * 4 + drow;
             const uint32_t kk = min(kv0k + row, a.kv_rows - 1);
             attn_dma(rk, lds0 + kstage * A_TILE + blk * 1024,
-                     (kk * a.ldk + ((dphys ^ (row & 15)) * 8)) * 2);
+                     (kk * a.ldk + ((dphys ^ (row & 15)) * 8)) * 2, 0);
             const uint32_t kvv = min(kv0v + row, a.kv_rows - 1);
             attn_dma(rv, lds0 + (2 + vstage) * A_TILE + blk * 1024,
-                     (kvv * a.ldv + ((dphys ^ (4 * (row & 3))) * 8)) * 2);
+                     (kvv * a.ldv + ((dphys ^ (4 * (row & 3))) * 8)) * 2, 0);
         }
     };
     /* S^T of one tile: keys kv0 + 32 kbk + [0, 32), one MFMA per 16-d step;
@@ -336,22 +357,23 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
      * (their readers passed the previous barrier), QK of tile t + 1, the
      * softmax and P.V of tile t, then wait for the issued tiles and
      * barrier. Past the end, loads are clamped and results unused. */
-    auto iter = [&](floatx16 (&sc)[AKB], floatx16 (&sn)[AKB], uint32_t t)
+    auto iter = [&](floatx16 (&sc)[AKB], floatx16 (&sn)[AKB], uint32_t t, auto odd)
         __attribute__((always_inline)) {
+        constexpr uint32_t st = decltype(odd)::value; /* t & 1, known at compile time */
         const uint32_t kv0 = t * AKT;
-        issue(t & 1, kv0 + 2 * AKT, (t + 1) & 1, kv0 + AKT);
+        issue(st, kv0 + 2 * AKT, st ^ 1, kv0 + AKT);
         bf16x8 pf[2 * AKB];
-        softmax_qk(sc, pf, kv0, (t + 1) & 1, sn);
-        pv(t & 1, pf);
+        softmax_qk(sc, pf, kv0, st ^ 1, sn);
+        pv(st, pf);
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): K(t + 2), V(t + 1) landed */
         attn_barrier();
     };
     uint32_t t = 0;
     for (; t + 1 < ntiles; t += 2) {
-        iter(s0, s1, t);
-        iter(s1, s0, t + 1);
+        iter(s0, s1, t, std::integral_constant<uint32_t, 0>());
+        iter(s1, s0, t + 1, std::integral_constant<uint32_t, 1>());
     }
-    if (t < ntiles) iter(s0, s1, t);
+    if (t < ntiles) iter(s0, s1, t, std::integral_constant<uint32_t, 0>());
 
     /* ---- normalise and store: o[db][v] = O[r][32 db + 8 (v/4) + 4 h + v%4] */
     attn_store_rows(a, o, l_run, b, r, head, h);
