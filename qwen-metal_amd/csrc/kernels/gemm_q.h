@@ -59,6 +59,15 @@ struct QgCtx {
 #define QG_MFMA0(acc, w, x) \
     asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(w), "v"(x))
 
+/* A VALU write of an MFMA operand needs 2 wait states before the MFMA that
+ * reads it, and the compiler does not see the asm MFMAs to insert them. This
+ * fence takes the fragments as inputs, so whatever writes them (int8
+ * widening, register copies) is placed before it, and supplies the 2. */
+__device__ __forceinline__ void qg_ready(const bf16x8 (&f)[8]) {
+    asm volatile("s_nop 1" ::"v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "v"(f[4]), "v"(f[5]),
+                 "v"(f[6]), "v"(f[7]));
+}
+
 /* fragment j of a sub-step, in the order its MFMAs consume them (W block 0,
  * A blocks 0-7, W blocks 1-7) */
 __device__ __forceinline__ void qg_read(const QgCtx &c, const unsigned char *cur, uint32_t ch,
@@ -120,6 +129,8 @@ __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
     bf16x8 af[8], bw[8], af1[8], bw1[8];
     u32x2 rw[8], rw1[8];
     if (PREV) {
+        qg_ready(pw);
+        qg_ready(pa);
 #pragma unroll
         for (int i = 0; i < 64; i++) {
             QG_MFMA(acc[i & 7][i >> 3], pw[i >> 3], pa[i & 7]);
@@ -138,6 +149,7 @@ __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
             for (int j = 0; j < 8; j++) bw[j] = i8x8_to_bf16(rw[j]);
         }
     }
+    if (INT8) qg_ready(bw);
 #pragma unroll
     for (int i = 0; i < 64; i++) {
         if (PREV)
@@ -229,6 +241,8 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
         qg_slice<INT8, true>(c, acc, pa, pw, lds_b, lds, kt * GBK);
         QW_SLICE_END();
     }
+    qg_ready(pw);
+    qg_ready(pa);
 #pragma unroll
     for (int i = 0; i < 64; i++) QG_MFMA(acc[i & 7][i >> 3], pw[i >> 3], pa[i & 7]);
     /* the epilogue reads the accumulators with ordinary instructions: let
@@ -266,6 +280,8 @@ __device__ __forceinline__ void qh_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
     };
     bf16x8 af[8], bw[8], af1[8], bw1[8];
     if (PREV) {
+        qg_ready(pw);
+        qg_ready(pa);
 #pragma unroll
         for (int i = 0; i < 32; i++) {
             QG_MFMA(acc[i & 3][i >> 2], pw[i >> 2], pa[i & 3]);
@@ -346,6 +362,8 @@ __device__ __forceinline__ void qh_mainloop(const qw_gemm_args &a, unsigned char
         qh_slice<true>(c, acc, pa, pw, lds_b, lds, kt * GBK);
         QW_SLICE_END();
     }
+    qg_ready(pw);
+    qg_ready(pa);
 #pragma unroll
     for (int i = 0; i < 32; i++) QG_MFMA(acc[i & 3][i >> 2], pw[i >> 2], pa[i & 3]);
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");

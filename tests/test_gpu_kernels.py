@@ -165,7 +165,7 @@ def test_linear_gelu_and_gate_epilogues(gpu, qd, oracle, int8, rows):
 # tile to finish adds the fp32 partials in piece order. 16 tiles with
 # k = 4096 are cut in 2; 10 ragged tiles (300 rows, 1032 columns) with
 # k = 8192 in 4; 12 tiles with k = 12288 (the MLP down projection's depth)
-# in 6.
+# in 6; 64 tiles with k = 8192 in 4 (256 pieces, one per CU).
 SPLIT_CASES = [
     (512, 4096, 2048, False, "store"),
     (300, 8192, 1032, True, "gelu"),
@@ -176,6 +176,9 @@ SPLIT_CASES = [
     (512, 8192, 2048, False, "gelu"),
     # int8 weights at >= 512 rows: widened first, then the bf16 kernels
     (512, 8192, 2048, True, "gate"),
+    # 64 tiles, 4 pieces each: every CU runs one piece; ragged, int8 widened
+    (2048, 8192, 2048, False, "gate"),
+    (2000, 8192, 2000, True, "gelu"),
 ]
 
 
