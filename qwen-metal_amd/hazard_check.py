@@ -20,8 +20,12 @@ branches), the wait states between:
   srcc->write  an MFMA reading a register as srcC and a VALU write of it: passes
   m0->lds      an SALU write of M0 and an LDS-direct load (``... lds``): 1
 
-(``s_nop N`` counts N + 1 wait states, every other instruction 1; passes:
-4x4 2, 16x16 8, 32x32 16.) An MFMA reading its own destination as srcC with
+(``s_nop N`` counts N + 1 wait states, every other instruction 1; passes
+as counted here: 4x4 2, 16x16 8, 32x32 16. These are upper bounds: for its
+own builtin MFMAs the compiler pads a VALU read of a 16x16x32 result with 8
+wait states, of a 32x32x16 result with 12, and an MFMA after a VALU write
+of its srcA with 1, so every limit here is at least the compiler's; the
+tests compile such a probe and check that.) An MFMA reading its own destination as srcC with
 the same register range chains in hardware and needs none. Exit status 1 and
 a listing when any distance is short.
 

@@ -99,3 +99,75 @@ def test_built_code_object_is_clean():
     assert any(any(x.lds_dma for x in v) for v in funcs.values())
     bad = hc.check(funcs)
     assert not bad, [(b[0], b[1], b[2], b[3], b[4].text, b[5].text) for b in bad[:5]]
+
+
+PROBE = r"""
+#include <hip/hip_runtime.h>
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+extern "C" __global__ void k16(const bf16x8 *a, float *o) {
+    floatx4 acc = {0, 0, 0, 0};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[threadIdx.x], a[threadIdx.x + 64], acc, 0, 0, 0);
+    o[threadIdx.x] = acc[0] * 3.0f;
+}
+extern "C" __global__ void k32(const bf16x8 *a, float *o) {
+    floatx16 acc = {};
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[threadIdx.x], a[threadIdx.x + 64], acc, 0, 0, 0);
+    o[threadIdx.x] = acc[0] * 3.0f;
+}
+extern "C" __global__ void kw(const bf16x8 *a, float *o) {
+    bf16x8 x = a[threadIdx.x];
+    x[0] = (__bf16)(o[threadIdx.x] * 2.0f);
+    floatx4 acc = {0, 0, 0, 0};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, a[threadIdx.x + 64], acc, 0, 0, 0);
+    o[threadIdx.x + 64] = acc[1];
+}
+"""
+
+
+def test_distances_not_below_the_compilers(tmp_path):
+    """The compiler pads its own (builtin) MFMAs with the wait states it
+    deems necessary; the scanner must demand at least as many. Probe: a
+    VALU read right after a 16x16x32 and a 32x32x16 result, and an MFMA
+    right after a VALU write of its srcA; the padding the compiler chose is
+    measured with the scanner's own distance walk."""
+    hipcc = os.path.join(os.path.dirname(hc.LLVM), "..", "bin", "hipcc")
+    hipcc = os.path.normpath(hipcc)
+    if not os.path.exists(hipcc):
+        pytest.skip("hipcc absent")
+    import subprocess
+    src, s = tmp_path / "probe.hip", tmp_path / "probe.s"
+    src.write_text(PROBE)
+    subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "--cuda-device-only", "-S",
+                    "-o", str(s), str(src)], check=True, capture_output=True)
+    # the assembly listing in llvm-objdump's layout: one function per kernel
+    text, addr, name = [], 0, None
+    for line in s.read_text().split("\n"):
+        body = line.split(";")[0].strip()
+        if body.endswith(":") and body[:-1] in ("k16", "k32", "kw"):
+            name = body[:-1]
+            text.append("%016x <%s>:" % (addr, name))
+            continue
+        if name is None or not body or body.startswith(".") or body.endswith(":"):
+            continue
+        text.append("\t%-58s// %012X: 00000000" % (body, addr))
+        addr += 4
+        if body.startswith("s_endpgm"):
+            name = None
+    funcs = hc.functions("\n".join(text) + "\n")
+    seen = {}
+    for fn, ins in funcs.items():
+        for x in ins:
+            if not x.mfma and x.srcs[0]:
+                for ws, y in hc._back(x, 40, lambda y: y.mfma and y.dst & x.srcs[0]):
+                    seen[(fn, "mfma->read")] = min(ws, seen.get((fn, "mfma->read"), 99))
+                    need = hc._passes(y.op) + hc.MFMA_EXTRA
+                    assert need >= ws, (fn, ws, need)
+            if x.mfma:
+                reads = set().union(*x.srcs)
+                for ws, y in hc._back(x, 12, lambda y: y.valu_write & reads):
+                    seen[(fn, "valu->mfma")] = min(ws, seen.get((fn, "valu->mfma"), 99))
+                    assert hc.VALU_WRITE_TO_MFMA >= ws, (fn, ws)
+    # the probe exercised every case (the compiler's padding: 8, 12 and 1)
+    assert {("k16", "mfma->read"), ("k32", "mfma->read"), ("kw", "valu->mfma")} <= set(seen)
