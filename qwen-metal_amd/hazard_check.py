@@ -25,8 +25,9 @@ as counted here: 4x4 2, 16x16 8, 32x32 16. These are upper bounds: for its
 own builtin MFMAs the compiler pads a VALU read of a 16x16x32 result with 8
 wait states, of a 32x32x16 result with 12, and an MFMA after a VALU write
 of its srcA with 1, so every limit here is at least the compiler's; the
-tests compile such a probe and check that.) An MFMA reading its own destination as srcC with
-the same register range chains in hardware and needs none. Exit status 1 and
+tests compile such a probe and check that.) An MFMA reading its own
+destination as srcC with the same register range chains in hardware and
+needs none. Exit status 1 and
 a listing when any distance is short.
 
 Usage: python hazard_check.py <code object .hsaco> [--max N]
