@@ -457,16 +457,21 @@ def ti2i_1024(qd, gpu, dit):
         _fields_ = [("rows", C.c_uint32), ("is_image", C.c_int), ("src_offset", C.c_uint32)]
     segs = (Seg * 4)(Seg(256, 0, 0), Seg(4096, 1, 0), Seg(64, 0, 256), Seg(4096, 1, 4096))
     rows = 256 + 4096 + 64 + 4096
+    err = C.create_string_buffer(1024)
     text = gpu.new(320 * CFG["text_dim"], qd.BF16)
     lat = gpu.new(8192 * CFG["z_dim"], qd.BF16)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, text.h, 0, text.n, SEED, 840, 1.0, 0.0), "fill")
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, lat.h, 0, lat.n, SEED, 841, 1.0, 0.0), "fill")
-    cos = np.empty((rows, 64), np.float32)
-    sin = np.empty((rows, 64), np.float32)
-    L.qw_pipe_rope_tables_host(rows - 4096, 64, 64, cos.ctypes.data, sin.ctypes.data)
-    ct, st = gpu.put(cos), gpu.put(sin)
+    # the reference's ti2i tables (qwen_pipeline.m:611-680): each block's
+    # text rows, then its 64 x 64 grid with the frame frozen where it starts
+    bh, bw, tb = (np.array(v, np.uint32) for v in ([64, 64], [64, 64], [256, 64]))
+    cp, sp = C.c_void_p(), C.c_void_p()
+    if not L.qw_pipe_rope_tables_blocks(gpu.h, bh.ctypes.data, bw.ctypes.data, tb.ctypes.data,
+                                        2, C.byref(cp), C.byref(sp), err, 1024):
+        raise RuntimeError(err.value.decode())
+    ct, st = qd.Tensor(gpu, cp.value, rows * 64, qd.F32), qd.Tensor(gpu, sp.value, rows * 64,
+                                                                   qd.F32)
     out = gpu.new(rows * CFG["z_dim"], qd.BF16)
-    err = C.create_string_buffer(1024)
 
     def run(sigma):
         if not L.qw_dit_forward_ti2i(dit.h, text.h, lat.h, segs, 4, 0, ct.h, st.h, sigma, out.h,

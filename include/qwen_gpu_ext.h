@@ -132,9 +132,13 @@ int qw_gpu_linear(h3_gpu *gpu, const qw_linear_desc *desc);
  * inside the GEMM loop (no bf16 staging copy); split tiles are used only as
  * far as their fp32 partials fit the buffer (at most 128 pieces), so long-K
  * linears may split less than qw_gpu_linear does (same bar: within one
- * bf16 ulp of it, or of its cancellation bound). A split that would need
- * more fails with an error. Calls on one GPU share that buffer: calls that
- * overlap on one GPU (several streams or threads at once) race. */
+ * bf16 ulp of it, or of its cancellation bound). Calls on one GPU share
+ * that buffer, whichever h3_gpu context or stream they come from: each call
+ * makes its stream wait for the previous call's kernels (a per-device event)
+ * and records its own, so calls issued one after another never overlap on
+ * the buffer (a stream under graph capture skips that wait: the captured
+ * graph's order is the caller's). The buffer keeps the last call's
+ * contents. */
 int qw_gpu_linear_static(h3_gpu *gpu, const qw_linear_desc *desc);
 
 /* Fused per-head RMSNorm (single rounding, h3_shaders.metal:4309-4329) and

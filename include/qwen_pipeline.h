@@ -43,6 +43,28 @@ int qw_pipe_rope_tables(h3_gpu *gpu, uint32_t text_rows, uint32_t gh,
 void qw_pipe_rope_tables_host(uint32_t text_rows, uint32_t gh, uint32_t gw,
                               float *cos_out, float *sin_out);
 
+/* reference qwen_pipeline.h:115-122 (qwen_pipeline.m:611-680): the ti2i
+ * multi-block tables. Block b is text_before[b] text rows, then a
+ * block_h[b] x block_w[b] image grid. One running position: a text row
+ * takes it on all three axes and advances it by 1; an image block's frame
+ * is the position where it starts, its rows sit on the grid centred as in
+ * qw_pipe_rope_tables, and the position then advances by max(h, w). Rows
+ * = sum text_before + sum h*w, 64 (cos, sin) pairs each. 0 with a message
+ * on an empty layout or a failed allocation. */
+int qw_pipe_rope_tables_blocks(h3_gpu *gpu, const uint32_t *block_h,
+                               const uint32_t *block_w,
+                               const uint32_t *text_before,
+                               uint32_t n_blocks, h3_gpu_tensor **rope_cos,
+                               h3_gpu_tensor **rope_sin, char *error,
+                               size_t error_size);
+/* Host-side form: fills [rows, 64] cos / sin (both NULL: only counts) and
+ * returns the row count. */
+size_t qw_pipe_rope_tables_blocks_host(const uint32_t *block_h,
+                                       const uint32_t *block_w,
+                                       const uint32_t *text_before,
+                                       uint32_t n_blocks, float *cos_out,
+                                       float *sin_out);
+
 /* reference qwen_pipeline.h:87-94. latents [gh*gw, 64] fp32 updated in
  * place. With guidance and neg_rows == text_rows the cond and uncond
  * branches run as ONE batch-2 forward (stacked rows); otherwise as two

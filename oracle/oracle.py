@@ -85,6 +85,8 @@ def lib():
                                           C.POINTER(C.c_float)]
         L.qo_rope_tables.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, f32p,
                                      f32p]
+        L.qo_rope_tables_blocks.restype = SZ
+        L.qo_rope_tables_blocks.argtypes = [u32p, u32p, u32p, C.c_uint32, f32p, f32p]
         L.qo_timestep_features.argtypes = [f32p, SZ, f32p]
         L.qo_synth_normal.restype = C.c_float
         L.qo_synth_normal.argtypes = [C.c_uint64, C.c_uint64, C.c_uint64]
@@ -223,6 +225,16 @@ def rope_tables(text_rows, gh, gw):
     c = np.empty((rows, 64), np.float32)
     s = np.empty((rows, 64), np.float32)
     lib().qo_rope_tables(text_rows, gh, gw, c, s)
+    return c, s
+
+
+def rope_tables_blocks(block_h, block_w, text_before):
+    """ti2i multi-block tables: [rows, 64] cos and sin"""
+    bh, bw, tb = (np.ascontiguousarray(x, np.uint32) for x in (block_h, block_w, text_before))
+    rows = int(tb.sum() + (bh.astype(np.int64) * bw).sum())
+    c = np.empty((rows, 64), np.float32)
+    s = np.empty((rows, 64), np.float32)
+    assert lib().qo_rope_tables_blocks(bh, bw, tb, len(bh), c, s) == rows
     return c, s
 
 

@@ -10,8 +10,8 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
-#ifdef _OPENMP
 #include <immintrin.h>
+#ifdef _OPENMP
 #include <omp.h>
 #endif
 
@@ -212,6 +212,46 @@ void qo_rope_tables(uint32_t text_rows, uint32_t gh, uint32_t gw,
                 sin_out[(size_t)t * 64 + col] = (float)sin(ang);
             }
     }
+}
+
+size_t qo_rope_tables_blocks(const uint32_t *block_h, const uint32_t *block_w,
+                             const uint32_t *text_before, uint32_t n_blocks,
+                             float *cos_out, float *sin_out) {
+    /* qwen_pipeline.m:611-680 (ti2i): text rows at (p, p, p) with p
+     * advancing by one per row; an image block of gh x gw at (frame, h -
+     * ceil(gh/2), w - ceil(gw/2)) with the frame frozen at the position the
+     * block starts at, after which the position advances by max(gh, gw).
+     * Angles in double, as qo_rope_tables. */
+    static const int dims[3] = {16, 56, 56};
+    double position = 0.0;
+    size_t r = 0;
+    for (uint32_t b = 0; b < n_blocks; b++) {
+        uint32_t rows_b = text_before[b] + block_h[b] * block_w[b];
+        long half_h = (long)(block_h[b] - block_h[b] / 2);
+        long half_w = (long)(block_w[b] - block_w[b] / 2);
+        double frame = position + (double)text_before[b];
+        for (uint32_t i = 0; i < rows_b; i++, r++) {
+            double pos[3];
+            if (i < text_before[b]) {
+                pos[0] = pos[1] = pos[2] = position + (double)i;
+            } else {
+                uint32_t idx = i - text_before[b];
+                pos[0] = frame;
+                pos[1] = (double)((long)(idx / block_w[b]) - half_h);
+                pos[2] = (double)((long)(idx % block_w[b]) - half_w);
+            }
+            size_t col = 0;
+            for (int a = 0; a < 3; a++)
+                for (int p = 0; p < dims[a] / 2; p++, col++) {
+                    double f = pow(10000.0, -2.0 * (double)p / (double)dims[a]);
+                    double ang = pos[a] * f;
+                    cos_out[r * 64 + col] = (float)cos(ang);
+                    sin_out[r * 64 + col] = (float)sin(ang);
+                }
+        }
+        position = frame + (double)(block_h[b] > block_w[b] ? block_h[b] : block_w[b]);
+    }
+    return r;
 }
 
 void qo_timestep_features(const float *sigmas, size_t count,

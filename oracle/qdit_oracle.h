@@ -17,6 +17,9 @@
  *                                 pipeline_fixture/schedule_*.f32 + _ref
  *   rope tables ................. dit_fixture a/b/c rope, pipeline_fixture
  *                                 rope_{4,8}, host_ref.json samples, _ref
+ *   rope tables, ti2i blocks .... hand-computed positions of a 3-block
+ *                                 layout; one block = the single-grid table
+ *                                 with its frame moved by the text rows
  *   timestep features ........... closed form (cos/sin of known angles)
  *   layer_norm_mod .............. dit_fixture a/b joint_in -> attn_in
  *   gate (+ layer_norm_mod) ..... dit_fixture attn_out/mlp_in/mlp_out/
@@ -89,6 +92,10 @@ void qo_rope_table_entry(int axis_dim, int table_row, int pair,
 /* qwen_pipeline.m:212-273: joint [text_rows + gh*gw, 64] tables */
 void qo_rope_tables(uint32_t text_rows, uint32_t gh, uint32_t gw,
                     float *cos_out, float *sin_out);
+/* ti2i multi-block tables (qwen_pipeline.m:611-680); returns the rows. */
+size_t qo_rope_tables_blocks(const uint32_t *block_h, const uint32_t *block_w,
+                             const uint32_t *text_before, uint32_t n_blocks,
+                             float *cos_out, float *sin_out);
 /* qwen_dit.m:1085-1096 */
 void qo_timestep_features(const float *sigmas, size_t count, float *features);
 

@@ -28,7 +28,8 @@ enum {
     /* GEMM kernels in QW_LINEAR_* epilogue order (store, gelu, gate, qknorm) */
     K_GEMM_BF16_STORE_Q, K_GEMM_BF16_GELU_Q, K_GEMM_BF16_GATE_Q, K_GEMM_BF16_QKN_Q,
     K_GEMM_I8_STORE_Q, K_GEMM_I8_GELU_Q, K_GEMM_I8_GATE_Q, K_GEMM_I8_QKN_Q, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
-    K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_ZERO, K_COUNT
+    K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_ZERO,
+    K_GEMM_W8_STORE_Q, K_GEMM_W8_GELU_Q, K_GEMM_W8_GATE_Q, K_GEMM_W8_QKN_Q, K_COUNT
 };
 static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_bf16", "qw_rms_norm_one_bf16", "qw_qk_norm_rope_bf16",
@@ -40,7 +41,13 @@ static const char *k_names[K_COUNT] = {
     "qw_widen_i8_bf16",
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16",
     "qw_gemv_bf16_store", "qw_gemv_bf16_gelu", "qw_gemv_i8_store", "qw_gemv_i8_gelu",
-    "qw_zero_u32"};
+    "qw_zero_u32",
+    "qw_gemm_w8_store_q", "qw_gemm_w8_gelu_q", "qw_gemm_w8_gate_q", "qw_gemm_w8_qkn_q"};
+
+/* int8 linears of QW_WIDEN_MIN_ROWS rows or more: widen the weight to a
+ * bf16 copy then run the bf16 kernels (WIDEN), or the int8 kernels that
+ * widen each fragment in every wave (I8), or once per workgroup (W8) */
+enum { QW_INT8_WIDEN = 0, QW_INT8_I8 = 1, QW_INT8_W8 = 2 };
 
 struct h3_gpu {
     int device;
@@ -56,6 +63,7 @@ struct h3_gpu {
     void *scratch;
     size_t scratch_bytes;
     uint32_t attn_threads; /* attention workgroup size, 64 per 32-query wave */
+    int int8_route; /* QW_INT8_* : how int8 linears of many rows run */
     void *widen; /* bf16 copy of the int8 weight of the linear in flight */
     size_t widen_bytes;
     uint32_t cus;      /* compute units */
@@ -155,6 +163,11 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     g->scratch_bytes = 0;
     g->widen = NULL;
     g->widen_bytes = 0;
+    g->int8_route = QW_INT8_WIDEN;
+    if (const char *r = getenv("QW_INT8_ROUTE")) {
+        if (!strcmp(r, "w8")) g->int8_route = QW_INT8_W8;
+        else if (!strcmp(r, "i8")) g->int8_route = QW_INT8_I8;
+    }
     g->cus = 0;
     g->sk_part = NULL;
     g->sk_flag = NULL;
@@ -830,6 +843,7 @@ static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps,
                              uint64_t max_pieces = (uint64_t)QW_SPLIT_MAX_PIECES * 1024u) {
     const uint32_t min_steps = 32;
     const uint32_t G = g->cus, R = tiles % G;
+    if (R == 0) return 1; /* every wave is full: nothing to split */
     uint32_t best = 1;
     double best_t = 0.9;
     for (uint32_t s = 2; s <= 8; s++) {
@@ -939,7 +953,8 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * 591-594 us (same box, alternating): the widening's VALU work does not
      * hide under the MFMAs. Fewer rows, and the allocation-free entry point,
      * use the int8 kernels. */
-    const int widen = int8 && !no_alloc && d->rows >= QW_WIDEN_MIN_ROWS;
+    const int widen =
+        int8 && !no_alloc && d->rows >= QW_WIDEN_MIN_ROWS && g->int8_route == QW_INT8_WIDEN;
     const void *wptr = d->weight->ptr;
     if (widen) {
         const size_t n = (size_t)d->cols * d->k, bytes = n * 2;
@@ -989,7 +1004,10 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * 149 / 155, up (GELU) 537 / 554, down 598 / 623; int8 weights in the
      * loop: 1941-1966 us for the four linears of a layer against 2009-2018
      * for the 8-wave int8 kernels. */
-    const int kid = (int8 && !widen ? K_GEMM_I8_STORE_Q : K_GEMM_BF16_STORE_Q) + d->epilogue;
+    const int kid = (!int8 || widen                   ? K_GEMM_BF16_STORE_Q
+                     : g->int8_route == QW_INT8_W8 ? K_GEMM_W8_STORE_Q
+                                                   : K_GEMM_I8_STORE_Q) +
+                    d->epilogue;
     const unsigned threads = 256, bm = 256, bn = 256;
     a.norm_q = qkn ? (const uint16_t *)d->norm_q->ptr : NULL;
     a.norm_k = qkn ? (const uint16_t *)d->norm_k->ptr : NULL;
@@ -1011,10 +1029,11 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
         if (s > 1) {
             const uint32_t R = tiles % g->cus;
             const size_t need = (size_t)R * s * QW_STATIC_PART_BYTES;
+            /* split_choice caps R s at QW_STATIC_PARTS and R < cus: an
+             * internal invariant, checked so a change to either fails loudly */
             if (need > (size_t)QW_STATIC_PARTS * QW_STATIC_PART_BYTES || R > QW_STATIC_FLAGS)
-                return fail(g, "linear_static: %u split pieces need %zu bytes of partials, over "
-                               "the static workspace's %u pieces", R * s, need,
-                            QW_STATIC_PARTS);
+                return fail(g, "linear_static: internal error: %u split pieces over the static "
+                               "workspace's %u", R * s, QW_STATIC_PARTS);
             uint32_t *flags = (uint32_t *)(g->static_scratch +
                                            (size_t)QW_STATIC_PARTS * QW_STATIC_PART_BYTES);
             /* the counters must start at zero: a previous call leaves them
@@ -1084,8 +1103,16 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
 extern "C" int qw_gpu_linear(h3_gpu *g, const qw_linear_desc *d) { return linear_impl(g, d, 0); }
 
 extern "C" int qw_gpu_linear_static(h3_gpu *g, const qw_linear_desc *d) {
-    if (g && !g->static_scratch) return fail(g, "linear_static: no static workspace");
-    return linear_impl(g, d, 1);
+    if (!g) return 0;
+    if (!g->static_scratch) return fail(g, "linear_static: no static workspace");
+    /* every context on this device shares the workspace: this call's
+     * kernels wait for the last call that used it, from any stream */
+    hipError_t e = (hipError_t)qw_static_scratch_acquire(g->device, g->stream);
+    if (e != hipSuccess) return fail(g, "linear_static: ordering: %s", hipGetErrorString(e));
+    const int ok = linear_impl(g, d, 1);
+    e = (hipError_t)qw_static_scratch_release(g->device, g->stream);
+    if (e != hipSuccess) return fail(g, "linear_static: ordering: %s", hipGetErrorString(e));
+    return ok;
 }
 
 static qw_linear_desc plain_linear(h3_gpu_tensor *out, const h3_gpu_tensor *in,

@@ -251,6 +251,278 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 
+/* int8 W widened once per workgroup (the "_w8" kernels): the bf16 kernel's
+ * pipeline and LDS layout, with the W stage filled by the workgroup itself
+ * instead of a direct load. Each thread owns 4 row pieces of the 256-row x
+ * 64-k int8 W tile (rows wave * 64 + 16 i + lane / 4, 16 bytes at k offset
+ * 16 (lane % 4)), loaded into registers (global -> VGPR, 16 KB per slice
+ * per workgroup: half the bf16 tile's bytes), widened to bf16 (exact) and
+ * written into the W stage with the bf16 tile's swizzle, so the fragment
+ * reads and MFMAs are the bf16 kernel's. Every weight element is widened
+ * once per workgroup (the "_i8" kernels widen each fragment in every wave
+ * that reads it, twice per element), and no widened copy goes through HBM.
+ *
+ * Timing, slice s (stage cur holds A(s), W(s); nxt receives slice s + 1):
+ * the held-back sub-step's MFMAs cover the 8 direct A loads of s + 1, the
+ * 16 fragment reads of sub-step 0, and then, piece by piece, the widening
+ * of W(s + 1) (its raw int8 loaded during slice s - 1) into nxt and the
+ * raw loads of W(s + 2) into the freed registers. The slice ends waiting
+ * for the A loads only (vmcnt(4): the 4 raw loads issued after them stay
+ * in flight across the barrier, a whole slice ahead of their use). The
+ * raw loads are inline assembly, like the direct loads, so their waits are
+ * explicit: before a piece is widened, the 11 memory operations issued
+ * after its load (3 later raw loads of the previous slice, this slice's 8
+ * direct loads, its c earlier reloads) may still be outstanding. */
+#define QW8_SLICE_END() asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory")
+
+__device__ __forceinline__ void qw8_load(u32x4 &r, u32x4 rsrc, uint32_t voff, uint32_t soff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(r) : "v"(voff), "s"(rsrc),
+                 "s"(soff));
+}
+/* the raw piece has landed once at most N memory operations remain
+ * outstanding; the piece is an operand, so its readers are placed after */
+template <int N>
+__device__ __forceinline__ void qw8_wait(u32x4 &r) {
+    asm volatile("s_waitcnt vmcnt(%1)" : "+v"(r) : "n"(N));
+}
+
+struct Qw8 {
+    u32x4 raw[4];
+    uint32_t voff[4];      /* raw piece i: byte offset of its row piece at k = 0 */
+    uint32_t wdst[4][2];   /* LDS byte offset (in a stage) of its two bf16 chunks */
+    float fa, fb;          /* widening temporaries */
+    uint32_t o[8];         /* the piece being widened, as packed bf16 pairs */
+};
+
+/* whole-piece widening (prologue) */
+__device__ __forceinline__ void qw8_widen(Qw8 &w, int i, unsigned char *stage) {
+    u32x4 lo, hi;
+    i8x16_to_bf16(w.raw[i], lo, hi);
+    *(u32x4 *)(stage + w.wdst[i][0]) = lo;
+    *(u32x4 *)(stage + w.wdst[i][1]) = hi;
+}
+
+/* byte B of x, sign-extended, to fp32 (exact) */
+template <int B>
+__device__ __forceinline__ float qw8_cvt(uint32_t x) {
+    float f;
+    if constexpr (B == 0)
+        asm volatile("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD "
+                     "src0_sel:BYTE_0" : "=v"(f) : "v"(x));
+    else if constexpr (B == 1)
+        asm volatile("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD "
+                     "src0_sel:BYTE_1" : "=v"(f) : "v"(x));
+    else if constexpr (B == 2)
+        asm volatile("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD "
+                     "src0_sel:BYTE_2" : "=v"(f) : "v"(x));
+    else
+        asm volatile("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD "
+                     "src0_sel:BYTE_3" : "=v"(f) : "v"(x));
+    return f;
+}
+__device__ __forceinline__ uint32_t qw8_pack(float lo, float hi) {
+    uint32_t o;
+    asm volatile("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(o) : "v"(lo), "v"(hi));
+    return o;
+}
+
+/* Step t (0..23) of widening raw piece p into stage `nxt`: per dword of the
+ * piece, two byte conversions, a pack, two conversions, a pack. The steps
+ * are inline assembly so each stays in the MFMA slot it is written in (the
+ * compiler would otherwise bunch a piece's 24 VALU instructions between two
+ * MFMAs and leave the matrix pipe idle). Step 0 waits for the raw piece;
+ * after step 23 the two bf16 chunks are stored and the piece's registers
+ * reloaded with the raw W of slice k_raw. */
+template <int P, int T>
+__device__ __forceinline__ void qw8_step(Qw8 &w, const QgCtx &c, unsigned char *nxt,
+                                         uint32_t k_raw) {
+    constexpr int D = T / 6, U = T % 6;
+    if constexpr (T == 0) qw8_wait<11>(w.raw[P]);
+#ifdef QW8_DIAG_NOCVT
+    if constexpr (T == 23) {
+        qw8_load(w.raw[P], c.w_rs4, w.voff[P], k_raw);
+        *(u32x4 *)(nxt + w.wdst[P][0]) = w.raw[P];
+        *(u32x4 *)(nxt + w.wdst[P][1]) = w.raw[P];
+    }
+    return;
+#endif
+    const uint32_t x = w.raw[P][D];
+    if constexpr (U == 0) w.fa = qw8_cvt<0>(x);
+    if constexpr (U == 1) w.fb = qw8_cvt<1>(x);
+    if constexpr (U == 2) w.o[2 * D] = qw8_pack(w.fa, w.fb);
+    if constexpr (U == 3) w.fa = qw8_cvt<2>(x);
+    if constexpr (U == 4) w.fb = qw8_cvt<3>(x);
+    if constexpr (U == 5) w.o[2 * D + 1] = qw8_pack(w.fa, w.fb);
+    if constexpr (T == 23) {
+        qw8_load(w.raw[P], c.w_rs4, w.voff[P], k_raw);
+        *(u32x4 *)(nxt + w.wdst[P][0]) = u32x4{w.o[0], w.o[1], w.o[2], w.o[3]};
+        *(u32x4 *)(nxt + w.wdst[P][1]) = u32x4{w.o[4], w.o[5], w.o[6], w.o[7]};
+    }
+}
+/* global step g (0..95) of a slice's widening: piece g / 24, step g % 24 */
+template <int G>
+__device__ __forceinline__ void qw8_g(Qw8 &w, const QgCtx &c, unsigned char *nxt,
+                                      uint32_t k_raw) {
+    if constexpr (G >= 0 && G < 96) qw8_step<G / 24, G % 24>(w, c, nxt, k_raw);
+}
+/* The 96 steps spread evenly over the MFMA slots [S0, 128) of a slice
+ * (slots 0-63: the held-back sub-step, 64-127: sub-step 0); the first slice
+ * of a tile has no held-back sub-step and spreads them over 64-127. */
+#ifndef QW8_S0
+#define QW8_S0 32
+#endif
+constexpr int qw8_start(int slot, int s0) {
+    return slot <= s0 ? 0 : slot >= 128 ? 96 : (slot - s0) * 96 / (128 - s0);
+}
+template <int SLOT, int S0>
+__device__ __forceinline__ void qw8_slot(Qw8 &w, const QgCtx &c, unsigned char *nxt,
+                                         uint32_t k_raw) {
+    constexpr int g0 = qw8_start(SLOT, S0), g1 = qw8_start(SLOT + 1, S0);
+    static_assert(g1 - g0 <= 3, "widening steps per MFMA slot");
+    if constexpr (g1 > g0) qw8_g<g0>(w, c, nxt, k_raw);
+    if constexpr (g1 > g0 + 1) qw8_g<g0 + 1>(w, c, nxt, k_raw);
+    if constexpr (g1 > g0 + 2) qw8_g<g0 + 2>(w, c, nxt, k_raw);
+}
+
+template <int I, bool PREV>
+__device__ __forceinline__ void qw8_loop1_at(const QgCtx &c, Qw8 &w, floatx4 (&acc)[8][8],
+                                             bf16x8 (&pa)[8], bf16x8 (&pw)[8], bf16x8 (&af)[8],
+                                             bf16x8 (&bw)[8], const unsigned char *cur,
+                                             unsigned char *nxt, uint32_t nl, uint32_t k_next,
+                                             uint32_t k_raw) {
+    QG_MFMA(acc[I & 7][I >> 3], pw[I >> 3], pa[I & 7]);
+    if constexpr ((I & 3) == 1 && (I >> 2) < 8)
+        gemm_dma16(c.a_rs4, nl + c.dst0 + (I >> 2) * 1024, c.a_dvoff[I >> 2], k_next * 2);
+    if constexpr ((I & 3) == 3) qg_read(c, cur, c.ch[0], af, bw, I >> 2);
+    qw8_slot<I, QW8_S0>(w, c, nxt, k_raw);
+    if constexpr (I + 1 < 64)
+        qw8_loop1_at<I + 1, PREV>(c, w, acc, pa, pw, af, bw, cur, nxt, nl, k_next, k_raw);
+}
+
+template <int I, bool PREV>
+__device__ __forceinline__ void qw8_loop2_at(const QgCtx &c, Qw8 &w, floatx4 (&acc)[8][8],
+                                             bf16x8 (&af)[8], bf16x8 (&bw)[8], bf16x8 (&af1)[8],
+                                             bf16x8 (&bw1)[8], const unsigned char *cur,
+                                             unsigned char *nxt, uint32_t k_raw) {
+    if constexpr (PREV)
+        QG_MFMA(acc[I & 7][I >> 3], bw[I >> 3], af[I & 7]);
+    else
+        QG_MFMA0(acc[I & 7][I >> 3], bw[I >> 3], af[I & 7]);
+    if constexpr ((I & 3) == 3) qg_read(c, cur, c.ch[1], af1, bw1, I >> 2);
+    qw8_slot<64 + I, PREV ? QW8_S0 : 64>(w, c, nxt, k_raw);
+    if constexpr (I + 1 < 64)
+        qw8_loop2_at<I + 1, PREV>(c, w, acc, af, bw, af1, bw1, cur, nxt, k_raw);
+}
+
+template <bool PREV>
+__device__ __forceinline__ void qw8_slice(const QgCtx &c, Qw8 &w, floatx4 (&acc)[8][8],
+                                          bf16x8 (&pa)[8], bf16x8 (&pw)[8],
+                                          const unsigned char *__restrict__ cur,
+                                          unsigned char *__restrict__ nxt, uint32_t k_next,
+                                          uint32_t k_raw) {
+    const uint32_t nl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)nxt;
+    bf16x8 af[8], bw[8], af1[8], bw1[8];
+    if constexpr (PREV) {
+        qg_ready(pw);
+        qg_ready(pa);
+        qw8_loop1_at<0, true>(c, w, acc, pa, pw, af, bw, cur, nxt, nl, k_next, k_raw);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            gemm_dma16(c.a_rs4, nl + c.dst0 + j * 1024, c.a_dvoff[j], k_next * 2);
+#pragma unroll
+        for (int j = 0; j < 16; j++) qg_read(c, cur, c.ch[0], af, bw, j);
+    }
+    qw8_loop2_at<0, PREV>(c, w, acc, af, bw, af1, bw1, cur, nxt, k_raw);
+#pragma unroll
+    for (int i = 0; i < 8; i++) pa[i] = af1[i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) pw[i] = bw1[i];
+}
+
+/* Sums of tile (tm, tn) over k-steps [kb, ke), int8 W widened per
+ * workgroup; ends with the LDS stages free and no load in flight. */
+__device__ __forceinline__ void qw8_mainloop(const qw_gemm_args &a, unsigned char *lds,
+                                             unsigned char *lds_b, uint32_t tm, uint32_t tn,
+                                             uint32_t kb, uint32_t ke, floatx4 (&acc)[8][8]) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    const uint32_t m0 = tm * 256, n0 = tn * 256;
+    QgCtx c;
+    Qw8 w;
+    const uint32_t lrow = lane >> 3, lp = lane & 7;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t r = wave * 64 + j * 8 + lrow;
+        c.a_dvoff[j] = (min(m0 + r, a.m - 1) * a.lda + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t r = wave * 64 + i * 16 + (lane >> 2), q = lane & 3;
+        w.voff[i] = min(n0 + r, a.n - 1) * a.k + q * 16;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            w.wdst[i][h] = QG_A_BYTES + r * 128 + (((2 * q + h) ^ ((r >> 1) & 7u)) << 4);
+    }
+    c.a_rs4 = gemm_rs4(a.a, a.a_bytes);
+    c.w_rs4 = gemm_rs4(a.w, a.w_bytes);
+    c.dst0 = wave * 64 * 128;
+    const uint32_t l16 = lane & 15, h = lane >> 4, swz = (l16 >> 1) & 7u;
+    c.a_frag = (wm * 128 + l16) * 128;
+    c.w_frag = (wn * 128 + l16) * 128;
+    c.ch[0] = ((0 + h) ^ swz) << 4;
+    c.ch[1] = ((4 + h) ^ swz) << 4;
+    const uint32_t KT = ke;
+    auto kraw = [&](uint32_t s) __attribute__((always_inline)) {
+        return (s < KT ? s : KT - 1) * GBK;
+    };
+    {
+        /* prologue: W(kb) raw, A(kb) direct, W(kb) widened into stage 0,
+         * then W(kb + 1) raw in flight */
+        const uint32_t nb =
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)lds;
+#pragma unroll
+        for (int i = 0; i < 4; i++) qw8_load(w.raw[i], c.w_rs4, w.voff[i], kb * GBK);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            gemm_dma16(c.a_rs4, nb + c.dst0 + j * 1024, c.a_dvoff[j], kb * GBK * 2);
+        asm volatile("s_waitcnt vmcnt(8)" : "+v"(w.raw[0]), "+v"(w.raw[1]), "+v"(w.raw[2]),
+                     "+v"(w.raw[3]));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            qw8_widen(w, i, lds);
+            qw8_load(w.raw[i], c.w_rs4, w.voff[i], kraw(kb + 1));
+        }
+    }
+    QW8_SLICE_END();
+    bf16x8 pa[8], pw[8];
+    qw8_slice<false>(c, w, acc, pa, pw, lds, lds_b, (kb + 1 < KT ? kb + 1 : kb) * GBK,
+                     kraw(kb + 2));
+    QW8_SLICE_END();
+    uint32_t kt = kb + 1;
+    for (; kt + 1 < KT; kt += 2) {
+        qw8_slice<true>(c, w, acc, pa, pw, lds_b, lds, (kt + 1) * GBK, kraw(kt + 2));
+        QW8_SLICE_END();
+        qw8_slice<true>(c, w, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK,
+                        kraw(kt + 3));
+        QW8_SLICE_END();
+    }
+    if (kt < KT) {
+        qw8_slice<true>(c, w, acc, pa, pw, lds_b, lds, kt * GBK, kraw(kt + 2));
+        QW8_SLICE_END();
+    }
+    /* the last raw loads (of slices never used) land before their
+     * registers can be given to anything else */
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(w.raw[0]), "+v"(w.raw[1]), "+v"(w.raw[2]),
+                 "+v"(w.raw[3]));
+    qg_ready(pw);
+    qg_ready(pa);
+#pragma unroll
+    for (int i = 0; i < 64; i++) QG_MFMA(acc[i & 7][i >> 3], pw[i >> 3], pa[i & 7]);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
 /* Half tiles (128 x 256, bf16 W): a tile walk whose last wave of tiles
  * would leave at least half the CUs idle runs those tiles as twice as many
  * half tiles instead. Same 2 x 2 waves, each 64 x 128 (4 x 8 MFMA tiles);
@@ -369,6 +641,18 @@ __device__ __forceinline__ void qh_mainloop(const qw_gemm_args &a, unsigned char
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 
+/* INT8: 0 bf16 W, 1 int8 W widened per fragment, 2 int8 W widened per
+ * workgroup */
+template <int INT8>
+__device__ __forceinline__ void qg_mainloop_any(const qw_gemm_args &a, unsigned char *lds,
+                                                unsigned char *lds_b, uint32_t tm, uint32_t tn,
+                                                uint32_t kb, uint32_t ke, floatx4 (&acc)[8][8]) {
+    if constexpr (INT8 == 2)
+        qw8_mainloop(a, lds, lds_b, tm, tn, kb, ke, acc);
+    else
+        qg_mainloop<INT8>(a, lds, lds_b, tm, tn, kb, ke, acc);
+}
+
 /* The epilogue of the tile (MB = 8) or half tile (MB = 4) whose rows start
  * at m0 and columns at n0: each wave's MB x 8 accumulator blocks. */
 template <int EPI, int INT8, int MB>
@@ -447,7 +731,7 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
                     uint32_t q = id;
                     if ((F & 7u) == 0) q = (q & 7u) * (F >> 3) + (q >> 3);
                     gemm_tile_at(a, q, tm, tn);
-                    qg_mainloop<INT8>(a, lds, lds_b, tm, tn, 0, KT, acc);
+                    qg_mainloop_any<INT8>(a, lds, lds_b, tm, tn, 0, KT, acc);
                     qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc);
                 } else if (!INT8) {
                     uint32_t hq = id - F;
@@ -463,7 +747,7 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
         }
         if ((ndp & 7u) == 0) pid = (pid & 7u) * (ndp >> 3) + (pid >> 3);
         gemm_tile_at(a, pid, tm, tn);
-        qg_mainloop<INT8>(a, lds, lds_b, tm, tn, 0, KT, acc);
+        qg_mainloop_any<INT8>(a, lds, lds_b, tm, tn, 0, KT, acc);
         qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc);
         return;
     }
@@ -475,7 +759,7 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
     const uint32_t piece = q / R, r = q % R;
     const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
     gemm_tile_at(a, ndp + r, tm, tn);
-    qg_mainloop<INT8>(a, lds, lds_b, tm, tn, kb, ke, acc);
+    qg_mainloop_any<INT8>(a, lds, lds_b, tm, tn, kb, ke, acc);
     float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
     qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc, slots + (size_t)piece * QW_SPLIT_PART);
     __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the partial's stores are done */
@@ -509,3 +793,8 @@ QG_ENTRY(qw_gemm_i8_store_q, QW_EPI_STORE, 1)
 QG_ENTRY(qw_gemm_i8_gelu_q, QW_EPI_GELU, 1)
 QG_ENTRY(qw_gemm_i8_gate_q, QW_EPI_GATE, 1)
 QG_ENTRY(qw_gemm_i8_qkn_q, QW_EPI_QKNORM, 1)
+/* int8 weights widened once per workgroup into the bf16 W stage */
+QG_ENTRY(qw_gemm_w8_store_q, QW_EPI_STORE, 2)
+QG_ENTRY(qw_gemm_w8_gelu_q, QW_EPI_GELU, 2)
+QG_ENTRY(qw_gemm_w8_gate_q, QW_EPI_GATE, 2)
+QG_ENTRY(qw_gemm_w8_qkn_q, QW_EPI_QKNORM, 2)

@@ -4,6 +4,8 @@
 #pragma once
 #include <stddef.h>
 
+#include <hip/hip_runtime.h>
+
 /* QW_STATIC_PARTS partials of one 256 x 256 fp32 tile (256 KiB each), then
  * QW_STATIC_FLAGS u32 counters: 32 MiB + 4 KiB per GPU, held until the
  * process ends. */
@@ -21,6 +23,14 @@ extern "C" {
  * current device) and cached per device. 0 on success, else a HIP error
  * code with a message in err. */
 int qw_static_scratch_address(int device, void **address, char *err, size_t err_size);
+/* Ordering of the workspace's users on one device, whatever context or
+ * stream they come from: acquire makes `stream` wait for the last call that
+ * used the workspace (an event recorded by release) and holds a per-device
+ * lock until release records this call's end on `stream`. Every call that
+ * launches kernels on the workspace runs between the two. 0 on success,
+ * else a HIP error code (acquire then holds nothing). */
+int qw_static_scratch_acquire(int device, hipStream_t stream);
+int qw_static_scratch_release(int device, hipStream_t stream);
 #ifdef __cplusplus
 }
 #endif

@@ -88,11 +88,87 @@ int qw_pipe_schedule(uint32_t steps, uint32_t seq_len, const double *turbo_sigma
     return 1;
 }
 
+/* one table row: the 64 (cos, sin) pairs of position (frame, h, w) over the
+ * axes (16, 56, 56), angle = position x 10000^(-2p / dim) in double */
+static void rope_row(const double pos[3], float *cos_row, float *sin_row) {
+    static const int dims[3] = {16, 56, 56};
+    size_t col = 0;
+    for (int a = 0; a < 3; a++)
+        for (int p = 0; p < dims[a] / 2; p++, col++) {
+            const double ang = pos[a] * pow(10000.0, -2.0 * (double)p / (double)dims[a]);
+            cos_row[col] = (float)cos(ang);
+            sin_row[col] = (float)sin(ang);
+        }
+}
+
+size_t qw_pipe_rope_tables_blocks_host(const uint32_t *block_h, const uint32_t *block_w,
+                                       const uint32_t *text_before, uint32_t n_blocks,
+                                       float *cos_out, float *sin_out) {
+    /* qwen_pipeline.m:611-680. One running position: each text row takes
+     * it on all three axes and advances it by one; an image block keeps its
+     * frame at the position it starts at, its rows sit on the centred grid
+     * (h - ceil(gh/2), w - ceil(gw/2)), and the position then advances by
+     * the block's longer side. */
+    double position = 0.0;
+    size_t row = 0;
+    for (uint32_t b = 0; b < n_blocks; b++) {
+        for (uint32_t t = 0; t < text_before[b]; t++, row++, position += 1.0) {
+            const double pos[3] = {position, position, position};
+            if (cos_out) rope_row(pos, cos_out + row * 64, sin_out + row * 64);
+        }
+        const uint32_t gh = block_h[b], gw = block_w[b];
+        const long ch = (long)(gh - gh / 2), cw = (long)(gw - gw / 2);
+        for (uint32_t y = 0; y < gh; y++)
+            for (uint32_t x = 0; x < gw; x++, row++) {
+                const double pos[3] = {position, (double)((long)y - ch),
+                                       (double)((long)x - cw)};
+                if (cos_out) rope_row(pos, cos_out + row * 64, sin_out + row * 64);
+            }
+        position += (double)(gh > gw ? gh : gw);
+    }
+    return row;
+}
+
+int qw_pipe_rope_tables_blocks(h3_gpu *gpu, const uint32_t *block_h, const uint32_t *block_w,
+                               const uint32_t *text_before, uint32_t n_blocks,
+                               h3_gpu_tensor **rope_cos, h3_gpu_tensor **rope_sin, char *error,
+                               size_t error_size) {
+    if (!rope_cos || !rope_sin || (n_blocks && (!block_h || !block_w || !text_before))) {
+        snprintf(error, error_size, "rope blocks: need the block arrays and two outputs");
+        return 0;
+    }
+    const size_t rows = qw_pipe_rope_tables_blocks_host(block_h, block_w, text_before, n_blocks,
+                                                        NULL, NULL);
+    if (!rows) {
+        snprintf(error, error_size, "rope blocks: empty layout");
+        return 0;
+    }
+    float *c = malloc(sizeof(float) * rows * 64), *s = malloc(sizeof(float) * rows * 64);
+    h3_gpu_tensor *ct = NULL, *st = NULL;
+    int ok = c && s;
+    if (ok) {
+        qw_pipe_rope_tables_blocks_host(block_h, block_w, text_before, n_blocks, c, s);
+        ct = h3_gpu_tensor_from_f32(gpu, c, rows * 64);
+        st = h3_gpu_tensor_from_f32(gpu, s, rows * 64);
+        ok = ct && st;
+    }
+    free(c);
+    free(s);
+    if (!ok) {
+        h3_gpu_tensor_free(ct);
+        h3_gpu_tensor_free(st);
+        snprintf(error, error_size, "rope blocks: host or device allocation failed");
+        return 0;
+    }
+    *rope_cos = ct;
+    *rope_sin = st;
+    return 1;
+}
+
 void qw_pipe_rope_tables_host(uint32_t text_rows, uint32_t gh, uint32_t gw, float *cos_out,
                               float *sin_out) {
     /* qwen_pipeline.m:212-273: axes (16, 56, 56), text row t at (t, t, t),
      * image row (h, w) at (text_rows, h - ceil(gh/2), w - ceil(gw/2)). */
-    static const int dims[3] = {16, 56, 56};
     const uint32_t rows = text_rows + gh * gw;
     const long ch = (long)(gh - gh / 2), cw = (long)(gw - gw / 2);
     for (uint32_t t = 0; t < rows; t++) {
@@ -105,13 +181,7 @@ void qw_pipe_rope_tables_host(uint32_t text_rows, uint32_t gh, uint32_t gw, floa
             pos[1] = (double)((long)(idx / gw) - ch);
             pos[2] = (double)((long)(idx % gw) - cw);
         }
-        size_t col = (size_t)t * 64;
-        for (int a = 0; a < 3; a++)
-            for (int p = 0; p < dims[a] / 2; p++, col++) {
-                const double ang = pos[a] * pow(10000.0, -2.0 * (double)p / (double)dims[a]);
-                cos_out[col] = (float)cos(ang);
-                sin_out[col] = (float)sin(ang);
-            }
+        rope_row(pos, cos_out + (size_t)t * 64, sin_out + (size_t)t * 64);
     }
 }
 

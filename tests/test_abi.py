@@ -82,6 +82,17 @@ def test_host_math_matches_oracle(qd, oracle):
     L.qw_pipe_rope_tables_host(23, 8, 8, c.ctypes.data, s_.ctypes.data)
     oc, os_ = oracle.rope_tables(23, 8, 8)
     assert np.array_equal(c, oc) and np.array_equal(s_, os_)
+    # ti2i multi-block tables: two condition images and the target
+    bh, bw, tb = (np.array(v, np.uint32) for v in ([12, 7, 16], [9, 7, 16], [30, 5, 11]))
+    rows = L.qw_pipe_rope_tables_blocks_host(bh.ctypes.data, bw.ctypes.data, tb.ctypes.data, 3,
+                                             None, None)
+    assert rows == int(tb.sum() + (bh * bw).sum())
+    cb = np.empty((rows, 64), np.float32)
+    sb = np.empty_like(cb)
+    assert L.qw_pipe_rope_tables_blocks_host(bh.ctypes.data, bw.ctypes.data, tb.ctypes.data, 3,
+                                             cb.ctypes.data, sb.ctypes.data) == rows
+    oc, os_ = oracle.rope_tables_blocks(bh, bw, tb)
+    assert np.array_equal(cb, oc) and np.array_equal(sb, os_)
     # pipeline schedule with mu = 1 (config 4: exp(mu) = e, no terminal)
     cfg = (C.c_byte * 64)()
     L.qw_sched_cfg_default(cfg)

@@ -1,6 +1,9 @@
 """Parity at the BASELINE.json configurations' full sizes, through the C-ABI,
 against the CPU oracle on the same seeded inputs.
 
+  configs[0]  one bf16 block, batch 1, 64 text + 256 image rows, hidden
+              3072, modulation from the timestep embedding at t = 0.5,
+              N(0, 1) activations: every row
   configs[1]  bf16 linear sweep at M = 4352, the four block shapes with bias
   configs[2]  block-causal prefix SDPA, batch 2 x 24 heads x (256 + 4096)
   configs[3]  the 32-layer bf16 model at 512^2 (1152 rows): every block, the
@@ -10,16 +13,20 @@ against the CPU oracle on the same seeded inputs.
               block of both branches, and the velocity
 
 Per-block criterion (north star): for each block, fed the GPU's own input
-to that block, the oracle's output on 512 sampled rows of each branch
-(every row still feeds K and V) against the GPU's: cosine >= 0.9999 and
-max-abs error within the bf16 noise band, i.e. at most 2x the max-abs
-difference between two oracle evaluations of the same block that differ
-only in the fp32 summation order of their contractions (K slices of 512 vs
-64), plus 2 bf16 ulps of the block's largest output. The 32-layer velocity
-is reported against the north star's relL2 1e-2; with random N(0, 0.02)
-weights two oracle runs differing only in summation order already sit at
-~1.5e-2 after 32 layers (measured in test_gpu_dit.py), so it is asserted
-at 2e-2 / cosine 0.9998 and the measured value is printed."""
+to that block, the oracle's output against the GPU's -- every row at
+configs[0] and configs[3], 512 sampled rows of each branch at configs[4]
+(every row still feeds K and V there) --: cosine >= 0.9999 and max-abs
+error within the bf16 noise band, i.e. at most 2x the max-abs difference
+between two oracle evaluations of the same block that differ only in the
+fp32 summation order of their contractions (K slices of 512 vs 64), plus 2
+bf16 ulps of the block's largest output.
+
+The 32-layer velocity: with random N(0, 0.02) weights, 32 chained blocks
+amplify single-ulp rounding flips, so the band of two oracle chains that
+differ only in that summation order is measured on the same inputs and the
+GPU's relL2 is held to max(1e-2, 1.15 x band) -- the north star's 1e-2
+wherever the band leaves room for it -- with cosine >= 0.9998; both
+numbers are printed."""
 import ctypes as C
 import math
 import sys
@@ -163,12 +170,13 @@ def qd_rope(gpu, T, gh, gw):
     return gpu.put(c), gpu.put(s)
 
 
-def _check_blocks(oracle, om, cfg, trace, mod, T, gh, gw, label, band_branch=0):
+def _check_blocks(oracle, om, cfg, trace, mod, T, gh, gw, label, band_branch=0,
+                  all_rows=False):
     """Every block of every branch: oracle on the GPU's input vs the GPU's
-    output, on the sampled rows."""
+    output, on the sampled rows (all_rows: on every row)."""
     H, Ls = cfg["hidden"], cfg["layers"]
     batch, R = trace.shape[1], trace.shape[2]
-    sample = _sample_rows(T, R)
+    sample = np.arange(R, dtype=np.uint32) if all_rows else _sample_rows(T, R)
     cos, sin = oracle.rope_tables(T, gh, gw)
     rm = (np.arange(R) < T).astype(np.uint32)
     f = oracle.bf16_to_f32
@@ -197,6 +205,23 @@ def _check_blocks(oracle, om, cfg, trace, mod, T, gh, gw, label, band_branch=0):
             assert mx <= allow, (layer, b, mx, band)
             worst = min(worst, (c, mx, band))
     return worst
+
+
+def _velocity_bound(oracle, om, cfg, text, T, lat, I, sigma, cos, sin, ref, label):
+    """The oracle's own 32-layer band on these inputs (K slices of 64
+    against the 512 of `ref`) and the bound max(1e-2, 1.15 x band)."""
+    lib = oracle.lib()
+    lib.qo_set_gemm_kc.argtypes = [C.c_size_t]
+    lib.qo_set_gemm_kc(64)
+    try:
+        alt = om.forward(text, T, lat, I, sigma, cos, sin, cfg["layers"])
+    finally:
+        lib.qo_set_gemm_kc(512)
+    f = oracle.bf16_to_f32
+    band = rel_l2(f(alt[T:]), f(ref[T:]))
+    bound = max(1e-2, 1.15 * band)
+    say(f"[{label}] oracle band (K slices 64 vs 512) relL2 {band:.4e} -> bound {bound:.4e}")
+    return band, bound
 
 
 # ---- configs[4]: the 1024^2 CFG int8 step --------------------------------------
@@ -243,7 +268,11 @@ def test_config4_velocity_32_layers(cfg4, oracle):
     g, w = f(c["out"][0][T:]), f(ref[T:])
     r, cs = rel_l2(g, w), cosine(g, w)
     say(f"[config4] velocity relL2 {r:.4e} (north star 1e-2) cos {cs:.7f}")
-    assert r <= 2e-2 and cs >= 0.9998
+    band, bound = _velocity_bound(oracle, c["om"], cfg, c["text"][:T * cfg["text_dim"]].copy(),
+                                  T, c["lat"][:I * cfg["z_dim"]].copy(), I, c["sigma"], cos,
+                                  sin, ref, "config4")
+    say(f"[config4] velocity relL2 {r:.4e} against band {band:.4e}, bound {bound:.4e}")
+    assert r <= bound and cs >= 0.9998
 
 
 # ---- the 512^2 32-layer bf16 loop -------------------------------
@@ -251,8 +280,8 @@ def test_config4_velocity_32_layers(cfg4, oracle):
 @pytest.mark.timeout(900)
 def test_config3_512_every_block_and_velocity(gpu, qd, oracle):
     """The 32-layer bf16 model at 512^2 (128 text + 1024 image rows, batch
-    1): every block against the oracle on its input, then the velocity
-    against the oracle's 32-layer chain."""
+    1): every row of every block against the oracle on its input, then the
+    velocity against the oracle's 32-layer chain and its band."""
     cfg = dict(FULL, int8_weights=0)
     T, gh, gw, sigma = 128, 32, 32, 1.0
     I = gh * gw
@@ -262,16 +291,19 @@ def test_config3_512_every_block_and_velocity(gpu, qd, oracle):
     trace, mod, out = _traced_forward(gpu, qd, cfg, SEED, 1, T, gh, gw, sigma, text, lat)
     om = oracle.Model(cfg, SEED, cfg["layers"])
     try:
-        _check_blocks(oracle, om, cfg, trace, mod, T, gh, gw, "config3")
+        _check_blocks(oracle, om, cfg, trace, mod, T, gh, gw, "config3", all_rows=True)
         cos, sin = oracle.rope_tables(T, gh, gw)
         ref = om.forward(text, T, lat, I, sigma, cos, sin, cfg["layers"])
+        band, bound = _velocity_bound(oracle, om, cfg, text, T, lat, I, sigma, cos, sin, ref,
+                                      "config3")
     finally:
         om.close()
     f = oracle.bf16_to_f32
     g, w = f(out[0][T:]), f(ref[T:])
     r, cs = rel_l2(g, w), cosine(g, w)
-    say(f"[config3] velocity relL2 {r:.4e} (north star 1e-2) cos {cs:.7f}")
-    assert r <= 2e-2 and cs >= 0.9998
+    say(f"[config3] velocity relL2 {r:.4e} against band {band:.4e}, bound {bound:.4e}, "
+        f"cos {cs:.7f}")
+    assert r <= bound and cs >= 0.9998
 
 
 @pytest.mark.timeout(600)
@@ -318,3 +350,58 @@ def test_config3_512_eight_step_loop(gpu, qd, oracle):
     assert np.array_equal(xd, x)
     dit.close()
     gpu.release()
+
+
+# ---- one block at 320 rows ------------------------------------------
+
+@pytest.mark.timeout(600)
+def test_config0_block_320_rows_bf16(gpu, qd, oracle):
+    """One bf16 block (layer 0) at batch 1, 64 text + 256 image rows (16 x 16
+    grid), hidden 3072, 24 x 128 heads, GELU-tanh MLP 12288, shift / scale /
+    gate: the modulation comes from the model's own conditioning at t = 0.5
+    (a 1-layer forward's trace), the block input is N(0, 1). qw_dit_block on
+    the GPU against qo_block on every one of the 320 rows, to the per-block
+    bar (cosine >= 0.9999, max-abs within the oracle's summation-order band
+    x 2 plus 2 bf16 ulps of the largest output)."""
+    cfg = dict(FULL, int8_weights=0, layers=1)
+    T, gh, gw, sigma = 64, 16, 16, 0.5
+    I, R, H = gh * gw, T + gh * gw, cfg["hidden"]
+    text = oracle.fill_normal_bf16(T * cfg["text_dim"], SEED, 930)
+    lat = oracle.fill_normal_bf16(I * cfg["z_dim"], SEED, 931)
+    say("[config0] modulation at t = 0.5 from a 1-layer traced forward")
+    _, mod, _ = _traced_forward(gpu, qd, cfg, SEED, 1, T, gh, gw, sigma, text, lat)
+    hid = oracle.fill_normal_bf16(R * H, SEED, 932)
+    cos, sin = oracle.rope_tables(T, gh, gw)
+    rm = (np.arange(R) < T).astype(np.uint32)
+    dit = qd.Dit(gpu, cfg, SEED)
+    try:
+        ht = gpu.put(hid)
+        say("[config0] qw_dit_block, 320 rows")
+        dit.block(0, ht, gpu.put(mod), gpu.put(cos), gpu.put(sin), gpu.put(rm), R, T)
+        gpu.submit()
+        got = ht.read().reshape(R, H)
+    finally:
+        dit.close()
+        gpu.release()
+    om = oracle.Model(cfg, SEED, 1)
+    lib = oracle.lib()
+    lib.qo_set_gemm_kc.argtypes = [C.c_size_t]
+    try:
+        want = hid.copy()
+        om.block(0, want, mod, cos, sin, rm, R, T)
+        lib.qo_set_gemm_kc(64)
+        alt = hid.copy()
+        om.block(0, alt, mod, cos, sin, rm, R, T)
+    finally:
+        lib.qo_set_gemm_kc(512)
+        om.close()
+    f = oracle.bf16_to_f32
+    g, w, a = (f(x).astype(np.float64).reshape(R, H) for x in (got, want, alt))
+    band = float(np.max(np.abs(a - w)))
+    allow = 2.0 * band + 2.0 * float(np.max(np.abs(w))) * 2.0 ** -8
+    c, mx = cosine(g, w), float(np.max(np.abs(g - w)))
+    say(f"[config0] every row: cos {c:.7f} max-abs {mx:.4g} (band {band:.4g}, allowed "
+        f"{allow:.4g}) relL2 {rel_l2(g, w):.2e}; text rows cos {cosine(g[:T], w[:T]):.7f}")
+    assert np.all(np.isfinite(g))
+    assert c >= 0.9999 and mx <= allow
+    assert cosine(g[:T], w[:T]) >= 0.9999 and cosine(g[T:], w[T:]) >= 0.9999

@@ -348,6 +348,72 @@ def test_ti2i_forward_and_step_cache(gpu, qd, oracle):
     m.close()
 
 
+@pytest.mark.timeout(900)
+def test_ti2i_1024_condition_hidden_3072(gpu, qd, oracle):
+    """ti2i at the north-star width (hidden 3072, 24 heads, GELU MLP 12288,
+    shift/scale/gate, biases, int8 weights; 4 blocks): 256 text rows, a
+    1024 x 1024 condition image (4096 rows), 64 text rows, the 1024 x 1024
+    target (4096 rows) -- 8512 joint rows. The RoPE tables come from
+    qw_pipe_rope_tables_blocks (qwen_pipeline.m:611-680) and equal the
+    oracle's bit for bit. The full pass matches the oracle's ti2i forward;
+    a second call with the cache (target rows only, against the cached K/V)
+    equals a fresh full pass at that sigma bit for bit, and matches the
+    oracle too. The cached step's target rows match the fresh full pass
+    to within fp32 summation order, not bit for bit: at 8512 rows the
+    down projection's last, partly filled wave of tiles is split into
+    k-ranges (summed as partials), at 4096 target rows it is not."""
+    import ctypes as C
+    c = dict(FULL, int8_weights=1, **BASE_VARIANT)
+    c["layers"] = 4
+    segs = [(256, 0, 0), (4096, 1, 0), (64, 0, 256), (4096, 1, 4096)]
+    rows, base = 8512, 8512 - 4096
+    L = qd.lib()
+    bh, bw, tb = (np.array(v, np.uint32) for v in ([64, 64], [64, 64], [256, 64]))
+    cp, sp = C.c_void_p(), C.c_void_p()
+    err = C.create_string_buffer(512)
+    assert L.qw_pipe_rope_tables_blocks(gpu.h, bh.ctypes.data, bw.ctypes.data, tb.ctypes.data,
+                                        2, C.byref(cp), C.byref(sp), err, 512), err.value
+    ct, st = qd.Tensor(gpu, cp.value, rows * 64, qd.F32), qd.Tensor(gpu, sp.value, rows * 64,
+                                                                   qd.F32)
+    cos, sin = oracle.rope_tables_blocks(bh, bw, tb)
+    assert np.array_equal(ct.read().reshape(rows, 64), cos)
+    assert np.array_equal(st.read().reshape(rows, 64), sin)
+    text = oracle.fill_normal_bf16(320 * c["text_dim"], 2026, 940)
+    lat = oracle.fill_normal_bf16(8192 * c["z_dim"], 2026, 941)
+    ins = [gpu.put(text), gpu.put(lat), ct, st]
+    dit = qd.Dit(gpu, c, 2026)
+    outs = [gpu.new(rows * c["z_dim"], qd.BF16) for _ in range(3)]
+    print("[ti2i 3072] full pass sigma 0.9, cached step sigma 0.4, full pass 0.4", flush=True)
+    ok, e = _ti2i_call(gpu, qd, dit, ins, segs, 1, 0.9, outs[0])
+    assert ok, e
+    ok, e = _ti2i_call(gpu, qd, dit, ins, segs, 1, 0.4, outs[1])  # cached
+    assert ok, e
+    qd.lib().qw_dit_ti2i_cache_clear(dit.h)
+    ok, e = _ti2i_call(gpu, qd, dit, ins, segs, 1, 0.4, outs[2])  # full again
+    assert ok, e
+    gpu.submit()
+    qd.lib().qw_dit_ti2i_cache_clear(dit.h)
+    dit.close()
+    g1, g2, g3 = (o.read().reshape(rows, c["z_dim"]) for o in outs)
+    f = oracle.bf16_to_f32
+    r23, c23 = rel_l2(f(g2[base:]), f(g3[base:])), cosine(f(g2[base:]), f(g3[base:]))
+    print(f"[ti2i 3072] cached vs full pass: relL2 {r23:.3e} cos {c23:.8f}, "
+          f"bit-exact {np.mean(g2[base:] == g3[base:]):.4f}", flush=True)
+    assert r23 < 5e-3 and c23 > 0.99999
+    m = oracle.Model(c, 2026, c["layers"])
+    try:
+        for sigma, got in ((0.9, g1), (0.4, g2), (0.4, g3)):
+            print(f"[ti2i 3072] oracle ti2i forward, sigma {sigma}", flush=True)
+            ref = m.forward_ti2i(text, 320, lat, 8192, segs, sigma, cos, sin, c["layers"])
+            r = rel_l2(f(got[base:]), f(ref[base:]))
+            cs = cosine(f(got[base:]), f(ref[base:]))
+            print(f"[ti2i 3072] sigma {sigma}: target rows relL2 {r:.3e} cos {cs:.7f}",
+                  flush=True)
+            assert r < 1e-2 and cs > 0.9999
+    finally:
+        m.close()
+
+
 def test_ti2i_rejects_bad_layouts(gpu, qd, oracle):
     c = cfg("small", **REF_VARIANT)
     ins = [gpu.new(20 * c["text_dim"], qd.BF16), gpu.new(80 * c["z_dim"], qd.BF16),

@@ -239,6 +239,36 @@ def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
     assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
+def test_linear_full_waves_never_split(qd, oracle):
+    """Every wave of tiles full (1024 tiles of 256 x 256: a whole number of
+    waves on any CU count dividing 1024, 256 on MI355X) with a long K
+    (4096): no tile is left for a split, so the runtime allocates no
+    split-tile workspace (a fresh context's allocated bytes do not move) and
+    the tile walk computes every tile whole; sampled rows against the
+    oracle to the linear bar."""
+    rows, k, n = 32768, 4096, 2048
+    gpu = qd.Gpu()
+    try:
+        x = synth(oracle, rows * k, 51)
+        w = synth(oracle, n * k, 52, 0.02)
+        xt, wt = gpu.put(x), gpu.put(w)
+        out = gpu.new(rows * n, qd.BF16)
+        gpu.submit()
+        before = gpu.stats().allocated_bytes
+        gpu.linear(out, xt, wt, rows, k, n)
+        gpu.submit()
+        assert gpu.stats().allocated_bytes == before
+        got = out.read().reshape(rows, n)
+    finally:
+        gpu.close()
+    pick = np.unique(np.linspace(0, rows - 1, 96).round().astype(np.int64))
+    xs = x.reshape(rows, k)[pick].copy()
+    ref = oracle.linear(xs, w, None, len(pick), k, n).ravel()
+    mag = oracle.bf16_to_f32(oracle.linear(xs & np.uint16(0x7FFF), w & np.uint16(0x7FFF), None,
+                                           len(pick), k, n)).ravel()
+    assert_linear_close(oracle, got[pick].ravel(), ref, mag)
+
+
 @pytest.mark.parametrize("epi", ["store", "gelu", "gate"])
 def test_linear_tile_walk(gpu, qd, oracle, epi):
     """More tiles than compute units: the 16x16x32 GEMM launches one

@@ -83,6 +83,50 @@ def test_rope_tables_dit_fixture(oracle, case, text, gh, gw):
     assert np.max(np.abs(sin - ref_s)) < 1e-5
 
 
+def _blocks_angle_rows(positions):
+    """the 64 (cos, sin) of each (frame, h, w) position, axes (16, 56, 56)"""
+    c = np.empty((len(positions), 64), np.float32)
+    s = np.empty_like(c)
+    for r, pos in enumerate(positions):
+        col = 0
+        for a, dim in enumerate((16, 56, 56)):
+            for p in range(dim // 2):
+                ang = pos[a] * 10000.0 ** (-2.0 * p / dim)
+                c[r, col], s[r, col] = math.cos(ang), math.sin(ang)
+                col += 1
+    return c, s
+
+
+def test_rope_tables_blocks_hand_positions(oracle):
+    """ti2i multi-block tables (qwen_pipeline.m:611-680) on a 3-block layout
+    whose positions are written out by hand: text rows advance one
+    position each, an image block's frame is the position it starts at,
+    its grid is centred at (ceil(h/2), ceil(w/2)), then the position jumps
+    by max(h, w)."""
+    text_before, bh, bw = [3, 2, 4], [2, 1, 4], [3, 1, 2]
+    pos = [(0, 0, 0), (1, 1, 1), (2, 2, 2),                       # text 0..2
+           (3, -1, -2), (3, -1, -1), (3, -1, 0),                   # 2 x 3 at frame 3
+           (3, 0, -2), (3, 0, -1), (3, 0, 0),
+           (6, 6, 6), (7, 7, 7),                                   # 3 + max(2, 3)
+           (8, -1, -1),                                            # 1 x 1 at frame 8
+           (9, 9, 9), (10, 10, 10), (11, 11, 11), (12, 12, 12),    # 8 + 1
+           (13, -2, -1), (13, -2, 0), (13, -1, -1), (13, -1, 0),   # 4 x 2 at frame 13
+           (13, 0, -1), (13, 0, 0), (13, 1, -1), (13, 1, 0)]
+    c, s = oracle.rope_tables_blocks(bh, bw, text_before)
+    wc, ws = _blocks_angle_rows(pos)
+    assert c.shape == (len(pos), 64)
+    assert np.array_equal(c, wc) and np.array_equal(s, ws)
+
+
+@pytest.mark.parametrize("text,gh,gw", [(0, 4, 4), (23, 8, 8), (64, 16, 12), (7, 5, 9)])
+def test_rope_tables_blocks_single_block_is_t2i_table(oracle, text, gh, gw):
+    """One block of `text` rows and a gh x gw grid is the t2i table
+    (qwen_pipeline.m:212-273), whose image frame is the text length."""
+    c, s = oracle.rope_tables_blocks([gh], [gw], [text])
+    rc, rs = oracle.rope_tables(text, gh, gw)
+    assert np.array_equal(c, rc) and np.array_equal(s, rs)
+
+
 def test_timestep_features_closed_form(oracle):
     feats = oracle.timestep_features([0.37, 0.0])
     # sigma = 0 -> cos 1, sin 0 everywhere; i = 0 -> frequency 1
