@@ -12,9 +12,9 @@ inputs are seeded synthetic data generated on the device (no checkpoint).
 Timed region: K forward steps (embed, conditioning, 32 blocks, final head)
 with every input already resident in HBM, bracketed by a device sync and
 hipEvents on the library's stream. The dominant kernel (the down-projection
-GEMM, M=8704 K=12288 N=3072, residual-gate epilogue, on the int8 weight
-widened to bf16) is timed the same way, on the same stream, for the
-roofline entry;
+GEMM, M=8704 K=12288 N=3072, residual-gate epilogue, int8 weight widened
+to bf16 in LDS inside the GEMM) is timed the same way, on the same stream,
+for the roofline entry;
 every other linear shape and the attention kernel are timed alongside for
 the breakdown.
 
@@ -41,6 +41,7 @@ PEAK_HBM_GBS = 8000.0
 CFG = dict(hidden=3072, heads=24, mlp_width=12288, text_dim=4096, z_dim=64, layers=32,
            mlp_act=1, adaln_shift=1, has_bias=1, text_causal=0, int8_weights=1)
 TEXT, GH, GW, BATCH, SIGMA, SEED = 256, 64, 64, 2, 0.5, 2026
+W8_MIN_K = 8192  # int8 linears with K >= this widen in LDS inside the GEMM ("_w8")
 
 
 def load_qdit():
@@ -76,9 +77,12 @@ def time_ms(gpu, fn, reps):
 
 def kernel_breakdown(qd, gpu, reps=10):
     """Each linear shape of the step and the attention kernel, alone, on the
-    library's stream. An int8 linear at these rows is two launches: the
-    weight widening (qw_widen_i8_bf16) and the bf16 GEMM with the scale in
-    its epilogue; both are also timed on their own."""
+    library's stream. `ms` is the int8 linear as the step runs it: the down
+    projection (K = 12288) is one launch of the "_w8" kernel, which widens
+    the int8 weight in LDS; the K = 3072 linears are two launches, the
+    weight widening pass (qw_widen_i8_bf16) and the bf16 GEMM with the scale
+    in its epilogue, both also timed on their own (`widen_ms`, `gemm_ms`;
+    for the down projection `gemm_ms` is the "_w8" launch itself)."""
     H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
     L = qd.lib()
     a = gpu.new(M * F, qd.BF16)
@@ -104,16 +108,21 @@ def kernel_breakdown(qd, gpu, reps=10):
         gemm = lambda: gpu.linear(big, a, wb, M, k, n, wscale=s, epilogue=epi, **kw)  # noqa
         full()
         ms = time_ms(gpu, full, reps)
-        widen()
-        widen_ms = time_ms(gpu, widen, reps)
-        gemm()
-        gemm_ms = time_ms(gpu, gemm, reps)
+        in_gemm = k >= W8_MIN_K  # the library's int8 route at these rows
+        if in_gemm:
+            gemm_ms, widen_ms = ms, 0.0
+        else:
+            widen()
+            widen_ms = time_ms(gpu, widen, reps)
+            gemm()
+            gemm_ms = time_ms(gpu, gemm, reps)
         fl = 2.0 * M * n * k
         res[name] = {"M": M, "K": k, "N": n, "ms": ms, "tflops": fl / ms / 1e9,
                      "frac_peak": fl / ms / 1e9 / PEAK_BF16_TFLOPS,
+                     "int8_route": "w8 (widened in LDS)" if in_gemm else "widening pass + bf16",
                      "gemm_ms": gemm_ms, "gemm_tflops": fl / gemm_ms / 1e9,
                      "widen_ms": widen_ms,
-                     "widen_gbs": 3.0 * n * k / widen_ms / 1e6}
+                     "widen_gbs": 3.0 * n * k / widen_ms / 1e6 if widen_ms else None}
         wb.free()
     qkv = gpu.new(M * 3 * H, qd.BF16)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, qkv.h, 0, M * 3 * H, 1, 3, 1.0, 0.0), "fill")
@@ -257,7 +266,7 @@ def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, calibrated against
     a copy kernel of known size), or None when it has not been measured."""
-    p = os.path.join(ROOT, "profiles", "gemm_down_bf16_gate_q_traffic.md")
+    p = os.path.join(ROOT, "profiles", "gemm_down_w8_gate_q_traffic.md")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -332,8 +341,8 @@ def profile_kernel(qd, gpu, reps=5):
     """Launch-only mode for rocprofv3 --pmc passes: a plain copy of a known
     size (the counter calibration: 256 MiB read + 256 MiB written), then
     the dominant GEMM -- the down projection, M=8704 K=12288 N=3072, on the
-    widened int8 weight with the residual-gate epilogue -- `reps` times.
-    Nothing is timed or printed as a result."""
+    int8 weight (qw_gemm_w8_gate_q, widened in LDS) with the residual-gate
+    epilogue -- `reps` times. Nothing is timed or printed as a result."""
     H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
     L = qd.lib()
     copy_elems = 128 << 20  # bf16: 256 MiB
@@ -346,11 +355,10 @@ def profile_kernel(qd, gpu, reps=5):
     wb, q, s = gpu.new(F * H, qd.BF16), gpu.new(F * H, qd.I8), gpu.new(H, qd.F32)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, wb.h, 0, F * H, 1, 2, 0.02, 0.0), "fill")
     gpu.check(L.h3_gpu_quantize_weight_int8(gpu.h, q.h, s.h, wb.h, H, F), "quant")
-    gpu.check(L.qw_gpu_widen_int8_bf16(gpu.h, wb.h, q.h, F * H), "widen")
     ep = epilogue_operands(qd, gpu, M, TEXT + GH * GW)
     out = gpu.new(M * H, qd.BF16)
     for _ in range(reps):
-        gpu.linear(out, a, wb, M, F, H, wscale=s, epilogue=qd.LINEAR_GATE,
+        gpu.linear(out, a, q, M, F, H, wscale=s, epilogue=qd.LINEAR_GATE,
                    **ep[qd.LINEAR_GATE])
     gpu.submit()
 
@@ -575,13 +583,15 @@ def main():
         roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
                     "traffic": measured_traffic(),
-                    "kernel": "qw_gemm_bf16_gate_q (down projection, M=8704 K=12288 N=3072, "
-                              "int8 weight widened by qw_widen_i8_bf16, scale and residual "
-                              "gate in the epilogue, tail tiles split in 3 k-ranges)",
+                    "kernel": "qw_gemm_w8_gate_q (down projection, M=8704 K=12288 N=3072, "
+                              "int8 weight widened to bf16 in LDS once per workgroup, scale "
+                              "and residual gate in the epilogue, tail tiles split in 3 "
+                              "k-ranges)",
                     "flop_per_launch": fl, "ms_per_launch": down["gemm_ms"],
-                    "algorithmic_bytes_per_launch": 2.0 * (down["M"] * down["K"] +
-                                                            down["N"] * down["K"] +
-                                                            2 * down["M"] * down["N"])}
+                    # A bf16 + W int8 + row scales + residual and output bf16
+                    "algorithmic_bytes_per_launch": (2.0 * down["M"] * down["K"] +
+                                                     down["N"] * down["K"] + 4.0 * down["N"] +
+                                                     4.0 * down["M"] * down["N"])}
     sweep = None if args.no_breakdown else sweep_4352(qd, gpu)
     blk = None if args.no_breakdown else block_320(qd, gpu)
     den = None if args.no_breakdown or args.no_denoise else denoise_512(qd, gpu)

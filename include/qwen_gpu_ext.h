@@ -96,10 +96,12 @@ enum { QW_LINEAR_STORE = 0, QW_LINEAR_GELU = 1, QW_LINEAR_GATE = 2, QW_LINEAR_QK
  *   y, then per-head RMS norm + RoPE on the q and k thirds (QKNORM)
  * weight is bf16 [cols, k] or int8 [cols, k] (then wscale f32 [cols] is
  * required; without wscale a bf16 weight is unscaled). Offsets/strides are
- * in elements; k must be a multiple of 64. An int8 linear of 512 or more
- * rows first widens the weight to bf16 (qw_gpu_widen_int8_bf16, into a
- * buffer the runtime keeps) and runs the bf16 GEMM with the scale in its
- * epilogue: the same sums, the same single rounding. */
+ * in elements; k must be a multiple of 64. An int8 weight is widened to
+ * bf16 inside the GEMM, once per workgroup into LDS, with the scale in the
+ * epilogue. Where that measured slower (512 or more rows, k < 8192) the
+ * weight is first widened to a bf16 copy (qw_gpu_widen_int8_bf16, into a
+ * buffer the runtime keeps) and the bf16 GEMM runs: the same sums, the
+ * same single rounding, the same bits. */
 typedef struct {
     h3_gpu_tensor *out;
     size_t out_offset;
@@ -128,8 +130,8 @@ int qw_gpu_linear(h3_gpu *gpu, const qw_linear_desc *desc);
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc): qw_gpu_linear with every workspace in
  * one static per-GPU device buffer of 32 MiB + 4 KiB, held until the
- * process ends. It calls no hipMalloc / hipFree. int8 weights are widened
- * inside the GEMM loop (no bf16 staging copy); split tiles are used only as
+ * process ends. It calls no hipMalloc / hipFree. int8 weights are always
+ * widened inside the GEMM (no bf16 staging copy); split tiles are used only as
  * far as their fp32 partials fit the buffer (at most 128 pieces), so long-K
  * linears may split less than qw_gpu_linear does (same bar: within one
  * bf16 ulp of it, or of its cancellation bound). Calls on one GPU share

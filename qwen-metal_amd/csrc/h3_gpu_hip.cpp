@@ -27,7 +27,7 @@ enum {
     K_REORDER, K_FILL, K_QUANT, K_DEQUANT, K_COPY2D, K_ATTN,
     /* GEMM kernels in QW_LINEAR_* epilogue order (store, gelu, gate, qknorm) */
     K_GEMM_BF16_STORE_Q, K_GEMM_BF16_GELU_Q, K_GEMM_BF16_GATE_Q, K_GEMM_BF16_QKN_Q,
-    K_GEMM_I8_STORE_Q, K_GEMM_I8_GELU_Q, K_GEMM_I8_GATE_Q, K_GEMM_I8_QKN_Q, K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
+    K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
     K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_ZERO,
     K_GEMM_W8_STORE_Q, K_GEMM_W8_GELU_Q, K_GEMM_W8_GATE_Q, K_GEMM_W8_QKN_Q, K_COUNT
 };
@@ -37,17 +37,18 @@ static const char *k_names[K_COUNT] = {
     "qw_modulation_reorder_bf16", "qw_fill_normal_bf16", "qw_quantize_int8_rows",
     "qw_dequant_int8_f32", "qw_copy2d", "qw_attention_bf16",
     "qw_gemm_bf16_store_q", "qw_gemm_bf16_gelu_q", "qw_gemm_bf16_gate_q", "qw_gemm_bf16_qkn_q",
-    "qw_gemm_i8_store_q", "qw_gemm_i8_gelu_q", "qw_gemm_i8_gate_q", "qw_gemm_i8_qkn_q",
     "qw_widen_i8_bf16",
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16",
     "qw_gemv_bf16_store", "qw_gemv_bf16_gelu", "qw_gemv_i8_store", "qw_gemv_i8_gelu",
     "qw_zero_u32",
     "qw_gemm_w8_store_q", "qw_gemm_w8_gelu_q", "qw_gemm_w8_gate_q", "qw_gemm_w8_qkn_q"};
 
-/* int8 linears of QW_WIDEN_MIN_ROWS rows or more: widen the weight to a
- * bf16 copy then run the bf16 kernels (WIDEN), or the int8 kernels that
- * widen each fragment in every wave (I8), or once per workgroup (W8) */
-enum { QW_INT8_WIDEN = 0, QW_INT8_I8 = 1, QW_INT8_W8 = 2 };
+/* How int8 linears run (QW_INT8_ROUTE, a measurement switch): AUTO (the
+ * default) widens the weight to a bf16 copy and runs the bf16 kernels when
+ * that measured faster -- 512+ rows and K < 8192 -- and otherwise runs the
+ * int8 kernels that widen each W tile once per workgroup in LDS; WIDEN and
+ * W8 force one route wherever it can run. */
+enum { QW_INT8_AUTO = 0, QW_INT8_WIDEN = 1, QW_INT8_W8 = 2 };
 
 struct h3_gpu {
     int device;
@@ -163,10 +164,10 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     g->scratch_bytes = 0;
     g->widen = NULL;
     g->widen_bytes = 0;
-    g->int8_route = QW_INT8_WIDEN;
+    g->int8_route = QW_INT8_AUTO;
     if (const char *r = getenv("QW_INT8_ROUTE")) {
         if (!strcmp(r, "w8")) g->int8_route = QW_INT8_W8;
-        else if (!strcmp(r, "i8")) g->int8_route = QW_INT8_I8;
+        else if (!strcmp(r, "widen")) g->int8_route = QW_INT8_WIDEN;
     }
     g->cus = 0;
     g->sk_part = NULL;
@@ -823,7 +824,7 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
     return widen_launch(g, (uint16_t *)out->ptr, (const int8_t *)q->ptr, count);
 }
 
-/* below this many rows an int8 linear widens in its GEMM loop instead */
+/* below this many rows an int8 linear always widens inside its GEMM */
 #define QW_WIDEN_MIN_ROWS 512
 
 /* Split tiles. A grid of one workgroup per 256 x 256 tile runs in waves of
@@ -860,7 +861,7 @@ static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps,
 }
 
 /* no_alloc: the workspace-free form behind qw_gpu_linear_static (int8
- * weights widen inside the GEMM loop; split-tile partials and counters live
+ * weights always widen inside the GEMM; split-tile partials and counters live
  * in the static workspace, as far as it holds them) */
 static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     if (!g || !d) return 0;
@@ -943,18 +944,23 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
         const uint32_t waves = (d->cols + 1) / 2; /* 2 columns per wave */
         return launch(g, kid, dim3((waves + 3) / 4), dim3(256), a);
     }
-    /* int8 weights with many rows: widen the weight to bf16 once (exact,
-     * unscaled) and run the bf16 GEMM, whose epilogue applies the per-row
-     * scale to the fp32 sums -- the same arithmetic as the int8 kernels,
-     * without their in-loop widening. At M = 8704 the int8 kernels (int8 W
-     * tiles in LDS, each fragment widened in registers between MFMAs) take
-     * 513-542 / 170-178 / 637-644 / 608-616 us for QKV / out / up / down,
-     * the widening pass plus the bf16 kernel 468-478 / 153-155 / 564-576 /
-     * 591-594 us (same box, alternating): the widening's VALU work does not
-     * hide under the MFMAs. Fewer rows, and the allocation-free entry point,
-     * use the int8 kernels. */
-    const int widen =
-        int8 && !no_alloc && d->rows >= QW_WIDEN_MIN_ROWS && g->int8_route == QW_INT8_WIDEN;
+    /* int8 weights: the "_w8" kernels widen each int8 W tile once per
+     * workgroup into the bf16 W stage in LDS (no copy through HBM, half
+     * the weight bytes). Where it measured faster -- 512+ rows and K <
+     * 8192 -- the weight is instead widened to a bf16 copy by one
+     * bandwidth-bound pass and the bf16 kernels run; both routes give the
+     * same bits (the per-row scale multiplies the finished fp32 sums). Same
+     * box, alternating, M = 8704, us (widening pass + bf16 kernel / w8):
+     * QKV 378-387 / 391-406, out 140-145 / 145-151, up 485-504 / 530-565,
+     * down 558-571 / 558-573; steps 66.30-66.49 ms with every int8 linear
+     * widened, 68.11-68.24 with every one on w8, 66.32-66.47 with w8 on the
+     * down projection only. The w8 kernels' extra cost is the widening's
+     * VALU work (1.5 instructions per weight per workgroup): the same
+     * kernel with the conversion left out runs as fast as the widening
+     * pass plus the bf16 kernel. */
+    int route = g->int8_route;
+    if (route == QW_INT8_AUTO) route = d->k >= 8192 ? QW_INT8_W8 : QW_INT8_WIDEN;
+    const int widen = int8 && !no_alloc && d->rows >= QW_WIDEN_MIN_ROWS && route == QW_INT8_WIDEN;
     const void *wptr = d->weight->ptr;
     if (widen) {
         const size_t n = (size_t)d->cols * d->k, bytes = n * 2;
@@ -995,19 +1001,12 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
         a.w_bytes = (uint32_t)wb;
         a.out_bytes = (uint32_t)ob;
     }
-    /* bf16 weights (or int8 widened above): the 16x16x32-MFMA kernels;
-     * int8 weights with few rows: the kernels that widen in their K loop */
     const int qkn = d->epilogue == QW_LINEAR_QKNORM;
     /* the 4-wave kernels (one wave per SIMD, 128 x 128 per wave). Same box,
      * alternating, M = 8704, us, against the 8-wave 16x16x32 kernels they
      * replaced (two waves per SIMD, 64 x 128 per wave): QKV 447 / 458, out
-     * 149 / 155, up (GELU) 537 / 554, down 598 / 623; int8 weights in the
-     * loop: 1941-1966 us for the four linears of a layer against 2009-2018
-     * for the 8-wave int8 kernels. */
-    const int kid = (!int8 || widen                   ? K_GEMM_BF16_STORE_Q
-                     : g->int8_route == QW_INT8_W8 ? K_GEMM_W8_STORE_Q
-                                                   : K_GEMM_I8_STORE_Q) +
-                    d->epilogue;
+     * 149 / 155, up (GELU) 537 / 554, down 598 / 623. */
+    const int kid = (int8 && !widen ? K_GEMM_W8_STORE_Q : K_GEMM_BF16_STORE_Q) + d->epilogue;
     const unsigned threads = 256, bm = 256, bn = 256;
     a.norm_q = qkn ? (const uint16_t *)d->norm_q->ptr : NULL;
     a.norm_k = qkn ? (const uint16_t *)d->norm_k->ptr : NULL;

@@ -1,7 +1,7 @@
 /* The linears' GEMM on CDNA4 matrix cores: out[m, n] = epi(sum_k A[m, k]
- * W[n, k]), W bf16 or int8 (the "_i8" kernels; per-row scale in the
- * epilogue), fp32 accumulation, issued as C^T = W A^T (W fragment as the A
- * operand).
+ * W[n, k]), W bf16 or int8 (the "_w8" kernels: widened to bf16 in LDS once
+ * per workgroup; per-row scale in the epilogue), fp32 accumulation, issued
+ * as C^T = W A^T (W fragment as the A operand).
  *
  * Geometry: a 256 x 256 tile per workgroup of 4 waves (2 x 2), one wave per
  * SIMD, each wave a 128 x 128 block of 8 x 8 v_mfma_f32_16x16x32_bf16 tiles
@@ -40,7 +40,6 @@ struct QgCtx {
     uint32_t wdst0;          /* the same for the W tile (half tiles: A has 32 rows per wave) */
     uint32_t a_frag, w_frag; /* fragment row base (rows + lane % 16) in bytes */
     uint32_t ch[2];          /* swizzled 16-byte chunk of sub-step 0 / 1 */
-    uint32_t w8[2];          /* int8 W: fragment byte offset of sub-step 0 / 1 */
 };
 
 /* acc += W-fragment x A-fragment, in place. The accumulator is an operand
@@ -84,81 +83,45 @@ __device__ __forceinline__ void qg_read(const QgCtx &c, const unsigned char *cur
  * into `nxt`. The slice's second sub-step is held back (its fragments in
  * pa, pw) and runs at the start of the next slice, after the barrier, while
  * that slice's direct loads and first fragments are issued: one direct load
- * and one fragment read every 4 MFMAs; under the 64 MFMAs of sub-step 0 the
- * 16 fragments of sub-step 1 are read, one every 4 MFMAs.
- *
- * int8 W (INT8): the W tile lands in LDS as int8 (256 rows x 64 B, half the
- * bytes of bf16: 4 direct loads per wave instead of 8); a W fragment is an
- * 8-byte read, widened to bf16 in registers 16 MFMAs after its read was
- * issued (its data has landed by then), so the widening's VALU work runs
- * between MFMAs instead of stalling them. The W fragments are read first in
- * each sub-step so that all 8 widen before the sub-step ends. */
-template <int INT8, bool PREV>
+ * and one fragment read every 4 MFMAs (measured 7-10% faster than the 16
+ * direct loads issued back to back, than the loads spread over both
+ * sub-steps, and than the read placed before the load); under the 64 MFMAs
+ * of sub-step 0 the 16 fragments of sub-step 1 are read, one every 4 MFMAs. */
+template <bool PREV>
 __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], bf16x8 (&pa)[8],
                                          bf16x8 (&pw)[8], const unsigned char *__restrict__ cur,
                                          unsigned char *__restrict__ nxt, uint32_t k_next) {
     const uint32_t nl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)nxt;
-    constexpr int NDMA = INT8 ? 12 : 16;
     auto dma = [&](int j) __attribute__((always_inline)) {
         if (j < 8)
             gemm_dma16(c.a_rs4, nl + c.dst0 + j * 1024, c.a_dvoff[j], k_next * 2);
-        else if (INT8)
-            gemm_dma16(c.w_rs4, nl + QG_A_BYTES + c.dst0 / 2 + (j - 8) * 1024, c.w_dvoff[j - 8],
-                       k_next);
         else
             gemm_dma16(c.w_rs4, nl + QG_A_BYTES + c.dst0 + (j - 8) * 1024, c.w_dvoff[j - 8],
                        k_next * 2);
     };
-    /* fragment j of sub-step ks: bf16 W in consumption order (W block 0, A
-     * blocks 0-7, W blocks 1-7); int8 W blocks 0-7 first, then A blocks 0-7 */
-    auto rd = [&](int ks, int j, bf16x8(&A)[8], bf16x8(&W)[8], u32x2(&RW)[8])
-                  __attribute__((always_inline)) {
-        if (INT8) {
-            if (j < 8)
-                RW[j] = *(const u32x2 *)(cur + QG_A_BYTES + c.w8[ks] + j * 1024);
-            else
-                A[j - 8] = *(const bf16x8 *)(cur + c.a_frag + (j - 8) * 2048 + c.ch[ks]);
-        } else {
-            qg_read(c, cur, c.ch[ks], A, W, j);
-        }
-    };
-    /* (one direct load and one fragment read every 4 MFMAs measured 7-10%
-     * faster than the 16 direct loads issued back to back, than the loads
-     * spread over both sub-steps, and than the read placed before the
-     * load) */
     bf16x8 af[8], bw[8], af1[8], bw1[8];
-    u32x2 rw[8], rw1[8];
     if (PREV) {
         qg_ready(pw);
         qg_ready(pa);
 #pragma unroll
         for (int i = 0; i < 64; i++) {
             QG_MFMA(acc[i & 7][i >> 3], pw[i >> 3], pa[i & 7]);
-            if ((i & 3) == 1 && (i >> 2) < NDMA) dma(i >> 2);
-            if ((i & 3) == 3) rd(0, i >> 2, af, bw, rw);
-            if (INT8 && (i & 3) == 3 && i >= 19 && ((i - 19) >> 2) < 8)
-                bw[(i - 19) >> 2] = i8x8_to_bf16(rw[(i - 19) >> 2]);
+            if ((i & 3) == 1) dma(i >> 2);
+            if ((i & 3) == 3) qg_read(c, cur, c.ch[0], af, bw, i >> 2);
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < NDMA; j++) dma(j);
+        for (int j = 0; j < 16; j++) dma(j);
 #pragma unroll
-        for (int j = 0; j < 16; j++) rd(0, j, af, bw, rw);
-        if (INT8) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) bw[j] = i8x8_to_bf16(rw[j]);
-        }
+        for (int j = 0; j < 16; j++) qg_read(c, cur, c.ch[0], af, bw, j);
     }
-    if (INT8) qg_ready(bw);
 #pragma unroll
     for (int i = 0; i < 64; i++) {
         if (PREV)
             QG_MFMA(acc[i & 7][i >> 3], bw[i >> 3], af[i & 7]);
         else
             QG_MFMA0(acc[i & 7][i >> 3], bw[i >> 3], af[i & 7]);
-        if ((i & 3) == 3) rd(1, i >> 2, af1, bw1, rw1);
-        if (INT8 && (i & 3) == 3 && i >= 19 && ((i - 19) >> 2) < 8)
-            bw1[(i - 19) >> 2] = i8x8_to_bf16(rw1[(i - 19) >> 2]);
+        if ((i & 3) == 3) qg_read(c, cur, c.ch[1], af1, bw1, i >> 2);
     }
 #pragma unroll
     for (int i = 0; i < 8; i++) pa[i] = af1[i];
@@ -168,7 +131,6 @@ __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
 
 /* Sums of tile (tm, tn) over k-steps [kb, ke) into acc; ends with the LDS
  * stages free (after a barrier). */
-template <int INT8>
 __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char *lds,
                                             unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                             uint32_t kb, uint32_t ke, floatx4 (&acc)[8][8]) {
@@ -182,18 +144,7 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
     for (int j = 0; j < 8; j++) {
         const uint32_t r = wave * 64 + j * 8 + lrow;
         c.a_dvoff[j] = (min(m0 + r, a.m - 1) * a.lda + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
-        if (!INT8)
-            c.w_dvoff[j] = (min(n0 + r, a.n - 1) * a.k + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
-    }
-    if (INT8) {
-        /* int8 W rows are 64 B: a direct load covers 16 rows; lane l lands on
-         * row l / 4, physical 16-byte chunk l % 4, which holds logical chunk
-         * (l % 4) ^ ((row / 4) % 4) */
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t r = wave * 64 + j * 16 + (lane >> 2);
-            c.w_dvoff[j] = min(n0 + r, a.n - 1) * a.k + ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
-        }
+        c.w_dvoff[j] = (min(n0 + r, a.n - 1) * a.k + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
     }
     c.a_rs4 = gemm_rs4(a.a, a.a_bytes);
     c.w_rs4 = gemm_rs4(a.w, a.w_bytes);
@@ -203,10 +154,6 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
     c.w_frag = (wn * 128 + l16) * 128;
     c.ch[0] = ((0 + h) ^ swz) << 4;
     c.ch[1] = ((4 + h) ^ swz) << 4;
-    /* int8 W fragment: 8-byte chunk 4 ks + lane / 16 of the row, at 8-byte
-     * slot chunk ^ 2 ((row / 4) % 4) (the 16-byte swizzle of the loads) */
-    c.w8[0] = (wn * 128 + l16) * 64 + ((h ^ (2 * ((l16 >> 2) & 3))) << 3);
-    c.w8[1] = (wn * 128 + l16) * 64 + (((4 + h) ^ (2 * ((l16 >> 2) & 3))) << 3);
     const uint32_t KT = ke;
     {
         const uint32_t nb =
@@ -214,31 +161,23 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
 #pragma unroll
         for (int j = 0; j < 8; j++)
             gemm_dma16(c.a_rs4, nb + c.dst0 + j * 1024, c.a_dvoff[j], kb * GBK * 2);
-        if (INT8) {
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                gemm_dma16(c.w_rs4, nb + QG_A_BYTES + c.dst0 / 2 + j * 1024, c.w_dvoff[j],
-                           kb * GBK);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                gemm_dma16(c.w_rs4, nb + QG_A_BYTES + c.dst0 + j * 1024, c.w_dvoff[j],
-                           kb * GBK * 2);
-        }
+        for (int j = 0; j < 8; j++)
+            gemm_dma16(c.w_rs4, nb + QG_A_BYTES + c.dst0 + j * 1024, c.w_dvoff[j], kb * GBK * 2);
     }
     QW_SLICE_END();
     bf16x8 pa[8], pw[8];
-    qg_slice<INT8, false>(c, acc, pa, pw, lds, lds_b, (kb + 1 < KT ? kb + 1 : kb) * GBK);
+    qg_slice<false>(c, acc, pa, pw, lds, lds_b, (kb + 1 < KT ? kb + 1 : kb) * GBK);
     QW_SLICE_END();
     uint32_t kt = kb + 1;
     for (; kt + 1 < KT; kt += 2) {
-        qg_slice<INT8, true>(c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
+        qg_slice<true>(c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
         QW_SLICE_END();
-        qg_slice<INT8, true>(c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
+        qg_slice<true>(c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
         QW_SLICE_END();
     }
     if (kt < KT) {
-        qg_slice<INT8, true>(c, acc, pa, pw, lds_b, lds, kt * GBK);
+        qg_slice<true>(c, acc, pa, pw, lds_b, lds, kt * GBK);
         QW_SLICE_END();
     }
     qg_ready(pw);
@@ -259,14 +198,17 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
  * per workgroup: half the bf16 tile's bytes), widened to bf16 (exact) and
  * written into the W stage with the bf16 tile's swizzle, so the fragment
  * reads and MFMAs are the bf16 kernel's. Every weight element is widened
- * once per workgroup (the "_i8" kernels widen each fragment in every wave
- * that reads it, twice per element), and no widened copy goes through HBM.
+ * once per workgroup (an earlier form widened each 8-byte fragment in
+ * registers in every wave that read it, twice per element: 8-10% slower
+ * than this on the step's shapes), and no widened copy goes through HBM.
  *
  * Timing, slice s (stage cur holds A(s), W(s); nxt receives slice s + 1):
  * the held-back sub-step's MFMAs cover the 8 direct A loads of s + 1, the
- * 16 fragment reads of sub-step 0, and then, piece by piece, the widening
- * of W(s + 1) (its raw int8 loaded during slice s - 1) into nxt and the
- * raw loads of W(s + 2) into the freed registers. The slice ends waiting
+ * 16 fragment reads of sub-step 0, and then, one VALU step per MFMA from
+ * MFMA QW8_S0 on, the widening of W(s + 1) (its raw int8 loaded during
+ * slice s - 1) into nxt and the raw loads of W(s + 2) into the freed
+ * registers (QW8_S0 must not be below 30: every direct load of the slice
+ * is issued before the first piece's wait). The slice ends waiting
  * for the A loads only (vmcnt(4): the 4 raw loads issued after them stay
  * in flight across the barrier, a whole slice ahead of their use). The
  * raw loads are inline assembly, like the direct loads, so their waits are
@@ -338,14 +280,6 @@ __device__ __forceinline__ void qw8_step(Qw8 &w, const QgCtx &c, unsigned char *
                                          uint32_t k_raw) {
     constexpr int D = T / 6, U = T % 6;
     if constexpr (T == 0) qw8_wait<11>(w.raw[P]);
-#ifdef QW8_DIAG_NOCVT
-    if constexpr (T == 23) {
-        qw8_load(w.raw[P], c.w_rs4, w.voff[P], k_raw);
-        *(u32x4 *)(nxt + w.wdst[P][0]) = w.raw[P];
-        *(u32x4 *)(nxt + w.wdst[P][1]) = w.raw[P];
-    }
-    return;
-#endif
     const uint32_t x = w.raw[P][D];
     if constexpr (U == 0) w.fa = qw8_cvt<0>(x);
     if constexpr (U == 1) w.fb = qw8_cvt<1>(x);
@@ -369,8 +303,9 @@ __device__ __forceinline__ void qw8_g(Qw8 &w, const QgCtx &c, unsigned char *nxt
  * (slots 0-63: the held-back sub-step, 64-127: sub-step 0); the first slice
  * of a tile has no held-back sub-step and spreads them over 64-127. */
 #ifndef QW8_S0
-#define QW8_S0 32
+#define QW8_S0 48 /* 48 and 32 within noise of each other, both ahead of 64 */
 #endif
+static_assert(QW8_S0 >= 30, "the first widening step waits on all 8 direct loads");
 constexpr int qw8_start(int slot, int s0) {
     return slot <= s0 ? 0 : slot >= 128 ? 96 : (slot - s0) * 96 / (128 - s0);
 }
@@ -641,16 +576,15 @@ __device__ __forceinline__ void qh_mainloop(const qw_gemm_args &a, unsigned char
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
 }
 
-/* INT8: 0 bf16 W, 1 int8 W widened per fragment, 2 int8 W widened per
- * workgroup */
+/* INT8: 0 bf16 W, 1 int8 W widened once per workgroup */
 template <int INT8>
 __device__ __forceinline__ void qg_mainloop_any(const qw_gemm_args &a, unsigned char *lds,
                                                 unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                                 uint32_t kb, uint32_t ke, floatx4 (&acc)[8][8]) {
-    if constexpr (INT8 == 2)
+    if constexpr (INT8)
         qw8_mainloop(a, lds, lds_b, tm, tn, kb, ke, acc);
     else
-        qg_mainloop<INT8>(a, lds, lds_b, tm, tn, kb, ke, acc);
+        qg_mainloop(a, lds, lds_b, tm, tn, kb, ke, acc);
 }
 
 /* The epilogue of the tile (MB = 8) or half tile (MB = 4) whose rows start
@@ -788,13 +722,9 @@ QG_ENTRY(qw_gemm_bf16_store_q, QW_EPI_STORE, 0)
 QG_ENTRY(qw_gemm_bf16_gelu_q, QW_EPI_GELU, 0)
 QG_ENTRY(qw_gemm_bf16_gate_q, QW_EPI_GATE, 0)
 QG_ENTRY(qw_gemm_bf16_qkn_q, QW_EPI_QKNORM, 0)
-/* int8 weights with the per-row scale, widened in registers */
-QG_ENTRY(qw_gemm_i8_store_q, QW_EPI_STORE, 1)
-QG_ENTRY(qw_gemm_i8_gelu_q, QW_EPI_GELU, 1)
-QG_ENTRY(qw_gemm_i8_gate_q, QW_EPI_GATE, 1)
-QG_ENTRY(qw_gemm_i8_qkn_q, QW_EPI_QKNORM, 1)
-/* int8 weights widened once per workgroup into the bf16 W stage */
-QG_ENTRY(qw_gemm_w8_store_q, QW_EPI_STORE, 2)
-QG_ENTRY(qw_gemm_w8_gelu_q, QW_EPI_GELU, 2)
-QG_ENTRY(qw_gemm_w8_gate_q, QW_EPI_GATE, 2)
-QG_ENTRY(qw_gemm_w8_qkn_q, QW_EPI_QKNORM, 2)
+/* int8 weights (per-row scale in the epilogue), widened once per workgroup
+ * into the bf16 W stage */
+QG_ENTRY(qw_gemm_w8_store_q, QW_EPI_STORE, 1)
+QG_ENTRY(qw_gemm_w8_gelu_q, QW_EPI_GELU, 1)
+QG_ENTRY(qw_gemm_w8_gate_q, QW_EPI_GATE, 1)
+QG_ENTRY(qw_gemm_w8_qkn_q, QW_EPI_QKNORM, 1)

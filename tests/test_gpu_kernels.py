@@ -239,6 +239,39 @@ def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
     assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
+@pytest.mark.parametrize("rows,k,n,epi", [(300, 3072, 1024, "gelu"), (1100, 12288, 768, "gate"),
+                                          (2000, 8192, 2000, "store")])
+def test_int8_in_gemm_widening_bit_identical(gpu, qd, oracle, rows, k, n, epi):
+    """The int8 kernels that widen each W tile once per workgroup in LDS
+    (taken below 512 rows and for K >= 8192) give the same bits as widening
+    the weight to a bf16 copy (qw_gpu_widen_int8_bf16) and running the bf16
+    kernel with the same row scales: the widening is exact and the scale
+    multiplies the finished fp32 sums in both. Split tiles included
+    (K = 8192 and 12288)."""
+    L = qd.lib()
+    x = synth(oracle, rows * k, 61)
+    w = synth(oracle, n * k, 62, 0.02)
+    b = synth(oracle, n, 63, 0.02)
+    q, sc = oracle.quantize_int8_rows(w, n, k)
+    xt, bt, qt, st = gpu.put(x), gpu.put(b), gpu.put(q), gpu.put(sc)
+    wide = gpu.new(n * k, qd.BF16)
+    gpu.check(L.qw_gpu_widen_int8_bf16(gpu.h, wide.h, qt.h, n * k), "widen")
+    E = {"store": qd.LINEAR_STORE, "gelu": qd.LINEAR_GELU, "gate": qd.LINEAR_GATE}[epi]
+    kw = {}
+    if epi == "gate":
+        mod = synth(oracle, 2 * 4 * n, 64, 0.3)
+        rm = (np.arange(rows) % 5 == 0).astype(np.uint32)
+        kw = dict(modulation=gpu.put(mod), row_map=gpu.put(rm), slots=4, gate_slot=3)
+    h0 = synth(oracle, rows * n, 65)
+    outs = []
+    for weight in (qt, wide):
+        out = gpu.put(h0)
+        gpu.linear(out, xt, weight, rows, k, n, bias=bt, wscale=st, epilogue=E, **kw)
+        gpu.submit()
+        outs.append(out.read())
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_linear_full_waves_never_split(qd, oracle):
     """Every wave of tiles full (1024 tiles of 256 x 256: a whole number of
     waves on any CU count dividing 1024, 256 on MI355X) with a long K
