@@ -44,6 +44,28 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+/* Sum over each 16-lane row of the wave, in every lane of the row: adds of
+ * the row rotated by 8, 4, 2 and 1 lanes (DPP row_ror: VALU, not the LDS
+ * crossbar a shuffle uses). The same bits as the xor-shuffle tree over
+ * 8, 4, 2, 1: after each step the partial sums repeat with that step's
+ * period, so lane i + n (mod 16) holds what lane i ^ n would, and every
+ * add pairs the same two operands. */
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xF, 0xF, false));
+    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xF, 0xF, false));
+    return v;
+}
+
+/* The per-head RMS-norm factor 1 / sqrt(mean of squares + eps) as the
+ * reference's kernel takes it (h3_shaders.metal:4323, Metal rsqrt): the
+ * hardware reciprocal square root, not a correctly rounded divide of a
+ * correctly rounded square root. */
+__device__ __forceinline__ float head_rms_inv(float sum_sq, float eps) {
+    return __builtin_amdgcn_rsqf(sum_sq * (1.0f / 128.0f) + eps);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

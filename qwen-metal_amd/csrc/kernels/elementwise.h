@@ -181,9 +181,8 @@ QW_KERNEL void __launch_bounds__(256) qw_qk_norm_rope_bf16(qw_qk_norm_rope_args 
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; i++) ss = fmaf(x[i], x[i], ss);
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-        const float inv = 1.0f / sqrtf(ss / 128.0f + a.eps);
+        ss = row16_sum(ss);
+        const float inv = head_rms_inv(ss, a.eps);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             x[2 * i] = bf2f(f2bf(x[2 * i] * inv * lo_bf(wn[i])));

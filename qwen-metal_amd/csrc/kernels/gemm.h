@@ -346,12 +346,10 @@ __device__ __forceinline__ void gemm_epilogue_mode(const qw_gemm_args &a, SlabWr
                     for (int j = 0; j < 8; j++) ss[i] = fmaf(y[i][j], y[i][j], ss[i]);
                 }
 #pragma unroll
-                for (int o = 8; o > 0; o >>= 1)
-#pragma unroll
-                    for (int i = 0; i < RP; i++) ss[i] += __shfl_xor(ss[i], o, 64);
+                for (int i = 0; i < RP; i++) ss[i] = row16_sum(ss[i]);
 #pragma unroll
                 for (int i = 0; i < RP; i++) {
-                    const float inv = 1.0f / sqrtf(ss[i] / 128.0f + a.eps);
+                    const float inv = head_rms_inv(ss[i], a.eps);
 #pragma unroll
                     for (int j = 0; j < 8; j++) y[i][j] = bf2f(f2bf(y[i][j] * inv * nw[j]));
 #pragma unroll
