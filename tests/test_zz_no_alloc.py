@@ -79,3 +79,53 @@ def test_linear_static_matches_linear(qd, oracle, k, n, int8, epi, m1, m2):
             _close(oracle, outs[True][i], outs[False][i], mag, epi)
     finally:
         gpu.close()
+
+
+def test_linear_static_two_contexts_in_flight(qd, oracle):
+    """Two contexts (two streams) on one GPU share the static workspace: the
+    second context's call is issued while the first one's split-tile linear
+    (K = 12288, its pieces' fp32 partials and counters in the workspace) is
+    still in flight, with no synchronisation between them. The per-device
+    ordering makes the second call wait for the first, so both outputs equal
+    those of the same calls run one at a time on the allocating entry
+    point, bit for bit (same split), and the workspace's counters are left
+    at zero (a third call matches too)."""
+    k, n, rows = 12288, 3072, 1152
+    gpus = [qd.Gpu(), qd.Gpu()]
+    try:
+        ins = []
+        for i, g in enumerate(gpus):
+            x = oracle.fill_normal_bf16(rows * k, SEED, 10 + i)
+            w = oracle.fill_normal_bf16(n * k, SEED, 20 + i, 0.02)
+            ins.append((g.put(x), g.put(w), g.new(rows * n, qd.BF16), g.new(rows * n, qd.BF16)))
+        for g in gpus:
+            g.submit()
+        # one at a time, allocating path, as the reference result
+        for g, (xt, wt, ref, _) in zip(gpus, ins):
+            g.linear(ref, xt, wt, rows, k, n)
+            g.submit()
+        # both static calls in flight together, then a third on the first context
+        for g, (xt, wt, _, out) in zip(gpus, ins):
+            g.linear(out, xt, wt, rows, k, n, no_alloc=True)
+        for g in gpus:
+            g.submit()
+        got = [out.read() for (_, _, _, out) in ins]
+        want = [ref.read() for (_, _, ref, _) in ins]
+        xt, wt, _, out = ins[0]
+        gpus[0].linear(out, xt, wt, rows, k, n, no_alloc=True)
+        gpus[0].submit()
+        again = out.read()
+    finally:
+        for g in gpus:
+            g.close()
+    mag = None
+    for i in range(2):
+        if not np.array_equal(got[i], want[i]):
+            # the static form may split into fewer pieces than the allocating
+            # one (its workspace holds 128): then the linear bar applies
+            x = oracle.fill_normal_bf16(rows * k, SEED, 10 + i)
+            w = oracle.fill_normal_bf16(n * k, SEED, 20 + i, 0.02)
+            mag = oracle.bf16_to_f32(oracle.linear(x & np.uint16(0x7FFF), w & np.uint16(0x7FFF),
+                                                   None, rows, k, n)).ravel()
+            _close(oracle, got[i], want[i], mag, "store")
+    assert np.array_equal(again, got[0])
