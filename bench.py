@@ -554,6 +554,10 @@ def main():
     out = gpu.new(BATCH * R * CFG["z_dim"], qd.BF16)
     gpu.submit()
     setup_s = time.time() - t0
+    # the CPU baseline first (host cores only, the device idle), so that the
+    # device work -- warm-up, the timed steps, the breakdown -- runs as one
+    # uninterrupted stretch at the end
+    cpu = None if args.no_cpu else cpu_baseline()
 
     step = lambda: dit.forward_batch(text, TEXT, lat, I, BATCH, SIGMA, cos_t, sin_t, out)  # noqa
     for _ in range(args.warmup):
@@ -596,7 +600,6 @@ def main():
     blk = None if args.no_breakdown else block_320(qd, gpu)
     den = None if args.no_breakdown or args.no_denoise else denoise_512(qd, gpu)
     ti2i = None if args.no_breakdown or args.no_denoise else ti2i_1024(qd, gpu, dit)
-    cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": "DiT ms/step @1024^2 (4352 tok, CFG b=2); linear+SDPA TFLOP/s & % MFMA peak",
         "value": ms_step, "unit": "ms/step", "n_gpus": 1, "steps": args.steps,

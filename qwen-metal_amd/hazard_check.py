@@ -1,8 +1,9 @@
 """Static check of the built gfx950 code object for the instruction-distance
 hazards that inline assembly hides from the compiler.
 
-The GEMM kernels issue their MFMAs, and all kernels their LDS-direct loads,
-from inline assembly. The compiler's hazard recognizer does not look inside
+The GEMM kernels issue their MFMAs, the int8 GEMMs their raw weight loads
+and widening conversions, and all kernels their LDS-direct loads, from
+inline assembly. The compiler's hazard recognizer does not look inside
 an asm statement, so the wait states that gfx9 requires between these
 instructions and the compiler's own are not guaranteed by construction; a
 schedule change can place, say, an accumulator write right before the MFMA
