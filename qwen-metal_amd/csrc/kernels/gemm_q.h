@@ -212,9 +212,10 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
  * for the A loads only (vmcnt(4): the 4 raw loads issued after them stay
  * in flight across the barrier, a whole slice ahead of their use). The
  * raw loads are inline assembly, like the direct loads, so their waits are
- * explicit: before a piece is widened, the 11 memory operations issued
- * after its load (3 later raw loads of the previous slice, this slice's 8
- * direct loads, its c earlier reloads) may still be outstanding. */
+ * explicit: before piece p is widened, the 11 memory operations issued
+ * after its load may still be outstanding (the 3 - p later raw loads of the
+ * previous slice, this slice's 8 direct loads, this slice's p earlier
+ * reloads). */
 #define QW8_SLICE_END() asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
 __device__ __forceinline__ void qw8_load(u32x4 &r, u32x4 rsrc, uint32_t voff, uint32_t soff) {
