@@ -243,7 +243,8 @@ def cfg4(gpu, qd, oracle):
 
 @pytest.mark.timeout(900)
 def test_config4_every_block_both_branches(cfg4, oracle):
-    """The production batch-2 forward (int8 widened route, split tiles,
+    """The production batch-2 forward (int8 widening pass for K = 3072, in-LDS
+    widening and split tiles for the down projection,
     persistent tile walk, fused q/k norm, 24-head SDPA at 4352 keys): each
     of the 32 blocks of each branch against qo_block on its input."""
     c = cfg4

@@ -83,7 +83,9 @@ LINEAR_CASES = [
     (300, 3072, 520, True, False),
     (256, 64, 3072, False, False),
     (513, 1024, 256, True, True),   # int8 widened to bf16 before the GEMM
-    (37, 256, 136, True, True),     # int8 widened inside the GEMM loop
+    (37, 256, 136, True, True),     # int8 widened in LDS inside the GEMM
+    (40, 64, 256, False, True),     # ... one K-slice: the prologue only
+    (100, 128, 520, True, True),    # ... two K-slices, ragged N
     (700, 512, 264, False, True),
     (2, 3072, 12288, True, False),
     # at most 8 rows: the streaming GEMV kernels (bf16 and int8 weights)
@@ -174,9 +176,9 @@ SPLIT_CASES = [
     # bf16 GELU and K >= 4096 stores run the 4-wave (one wave per SIMD)
     # kernels: their split-tile path
     (512, 8192, 2048, False, "gelu"),
-    # int8 weights at >= 512 rows: widened first, then the bf16 kernels
+    # int8 weights with K >= 8192: widened in LDS inside the GEMM, split
     (512, 8192, 2048, True, "gate"),
-    # 64 tiles, 4 pieces each: every CU runs one piece; ragged, int8 widened
+    # 64 tiles, 4 pieces each: every CU runs one piece; ragged, int8 in LDS
     (2048, 8192, 2048, False, "gate"),
     (2000, 8192, 2000, True, "gelu"),
 ]

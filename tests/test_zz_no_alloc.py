@@ -28,7 +28,7 @@ CASES = [
     # K = 12288: split tiles in both entry points (static: fewer pieces)
     (12288, 3072, False, "store", 1152, 600),
     # int8: qw_gpu_linear widens to bf16 first (>= 512 rows), the static
-    # form widens inside the GEMM loop
+    # form widens in LDS inside the GEMM
     (3072, 1536, True, "gelu", 1100, 520),
     (3072, 3072, True, "gate", 700, 64),
 ]
