@@ -157,12 +157,14 @@ QW_KERNEL void __launch_bounds__(256) qw_gemv_i8_gelu(qw_gemm_args a) {
 
 /* Workgroup id -> (tile row, tile column). Ids are dealt round-robin to the
  * 8 XCDs; the id is remapped so each XCD owns a contiguous range of tiles,
- * walked in groups of 8 tile-rows (column-major inside a group), so the A
+ * walked in groups of 4 tile-rows (column-major inside a group), so the A
  * and W panels an XCD touches stay hot in its L2. */
 __device__ __forceinline__ void gemm_tile_at(const qw_gemm_args &a, uint32_t pid, uint32_t &tm,
                                              uint32_t &tn) {
 #ifndef QW_GEMM_GROUP
-#define QW_GEMM_GROUP 8
+/* 4 against 8 (same box, alternating, M = 8704): QKV 381 / 388, out 150 /
+ * 152, up 509 / 514, down 572 / 578 us (medians), steps 66.15 / 66.62 ms */
+#define QW_GEMM_GROUP 4
 #endif
     const uint32_t G = QW_GEMM_GROUP;
     const uint32_t per_group = G * a.tiles_n;
