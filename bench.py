@@ -11,12 +11,13 @@ inputs are seeded synthetic data generated on the device (no checkpoint).
 
 Timed region: K forward steps (embed, conditioning, 32 blocks, final head)
 with every input already resident in HBM, bracketed by a device sync and
-hipEvents on the library's stream. The dominant kernel (the down-projection
-GEMM, M=8704 K=12288 N=3072, residual-gate epilogue, int8 weight widened
-to bf16 in LDS inside the GEMM) is timed the same way, on the same stream,
-for the roofline entry;
-every other linear shape and the attention kernel are timed alongside for
-the breakdown.
+hipEvents on the library's stream. Right after it, the same forwards run
+with a HIP event pair around every stage of every block on that stream
+(`in_step`, no synchronisation inside a forward); the dominant kernel's
+average there (the down-projection GEMM, M=8704 K=12288 N=3072,
+residual-gate epilogue, int8 weight widened to bf16 in LDS inside the GEMM)
+is the roofline entry's launch time. Every linear shape and the attention
+kernel are also timed alone, back to back, for the breakdown.
 
 cpu_baseline: the CPU oracle (oracle/, OpenMP) on BASELINE configs[0]-[2]
 (block, linear sweep, SDPA; 1 warm-up + median of 5), composed to a step.
@@ -134,6 +135,49 @@ def kernel_breakdown(qd, gpu, reps=10):
     _, sd, _ = flops(dict(CFG, layers=1), R, TEXT, BATCH)
     res["attention"] = {"batch": BATCH, "q_rows": R, "heads": CFG["heads"], "ms": ms,
                         "tflops": sd / ms / 1e9, "frac_peak": sd / ms / 1e9 / PEAK_BF16_TFLOPS}
+    return res
+
+
+SPAN_NAMES = ["ln1", "qkv", "attention", "out", "ln2", "up", "down"]  # QW_SPAN_* order
+
+
+def stage_spans(qd, gpu, dit, step, steps):
+    """Each stage of every block as the step runs it: `steps` forwards of
+    the workload right after the timed region, with a HIP event pair per
+    stage recorded on the library's stream (qw_dit_set_spans; no
+    synchronisation inside a forward). Average device ms per launch, and
+    for the linears and attention their FLOP rate."""
+    import ctypes as C
+    L = qd.lib()
+    H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
+    gpu.check(L.qw_dit_set_spans(dit.h, 1), "spans on")
+    acc = {n: [] for n in SPAN_NAMES}
+    tags = (C.c_int * 4096)()
+    ms = (C.c_double * 4096)()
+    try:
+        gpu.submit()
+        L.qw_gpu_span_collect(gpu.h, tags, ms, 4096)  # nothing pending
+        for _ in range(steps):
+            step()
+            n = L.qw_gpu_span_collect(gpu.h, tags, ms, 4096)
+            if n < 0:
+                raise RuntimeError(gpu.error())
+            for i in range(n):
+                acc[SPAN_NAMES[tags[i]]].append(ms[i])
+    finally:
+        gpu.check(L.qw_dit_set_spans(dit.h, 0), "spans off")
+    _, sd, _ = flops(dict(CFG, layers=1), TEXT + GH * GW, TEXT, BATCH)
+    fl = {"qkv": 2.0 * M * H * 3 * H, "out": 2.0 * M * H * H, "up": 2.0 * M * H * F,
+          "down": 2.0 * M * F * H, "attention": sd}
+    res = {"steps": steps, "launches_per_stage": len(acc["down"])}
+    for n, v in acc.items():
+        avg = sum(v) / len(v)
+        res[n] = {"ms": avg}
+        if n in fl:
+            res[n]["tflops"] = fl[n] / avg / 1e9
+            res[n]["frac_peak"] = fl[n] / avg / 1e9 / PEAK_BF16_TFLOPS
+        else:
+            res[n]["gbs"] = 4.0 * M * H / avg / 1e6  # read + write of [M, H] bf16
     return res
 
 
@@ -574,16 +618,19 @@ def main():
     v = out.read().view(np.uint16)
     finite = bool(np.all((v & 0x7F80) != 0x7F80))
 
+    in_step = stage_spans(qd, gpu, dit, step, min(args.steps, 10))
     lin, sdpa, extra = flops(CFG, R, TEXT, BATCH)
     total_tflops = (lin + sdpa + extra) / ms_step / 1e9
     brk = {} if args.no_breakdown else kernel_breakdown(qd, gpu)
-    down = brk.get("down")
+    down = dict(M=BATCH * R, K=CFG["mlp_width"], N=CFG["hidden"], ms=in_step["down"]["ms"])
     roofline = None
     if down:
         # the dominant kernel of the step (largest total time in the kernel
-        # trace): the down projection's GEMM
+        # trace): the down projection's GEMM, one launch per block, its
+        # average over the blocks of the forwards right after the timed
+        # region (HIP events on the library's stream)
         fl = 2.0 * down["M"] * down["N"] * down["K"]
-        achieved = fl / down["gemm_ms"] / 1e9
+        achieved = fl / down["ms"] / 1e9
         roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
                     "traffic": measured_traffic(),
@@ -591,7 +638,8 @@ def main():
                               "int8 weight widened to bf16 in LDS once per workgroup, scale "
                               "and residual gate in the epilogue, tail tiles split in 3 "
                               "k-ranges)",
-                    "flop_per_launch": fl, "ms_per_launch": down["gemm_ms"],
+                    "flop_per_launch": fl, "ms_per_launch": down["ms"],
+                    "ms_per_launch_alone": brk["down"]["gemm_ms"] if brk else None,
                     # A bf16 + W int8 + row scales + residual and output bf16
                     "algorithmic_bytes_per_launch": (2.0 * down["M"] * down["K"] +
                                                      down["N"] * down["K"] + 4.0 * down["N"] +
@@ -613,6 +661,7 @@ def main():
         "step_tflops": total_tflops,
         "step_frac_peak": total_tflops / PEAK_BF16_TFLOPS,
         "flop_per_step": {"linear": lin, "sdpa": sdpa, "other": extra},
+        "in_step": in_step,
         "breakdown": brk,
         "sweep_4352_bf16": sweep,
         "block_320_bf16": blk,

@@ -245,6 +245,18 @@ int qw_dit_forward_batch_features(qw_dit *dit, const h3_gpu_tensor *text_in,
  * conditioning and final. Returns the number of stages written. */
 int qw_dit_block_profile(const qw_dit *dit, double *ms, int max_stages);
 
+/* No counterpart in the reference (a measurement aid): while on, every
+ * block records one qw_gpu_span (qwen_gpu_ext.h) per stage on the
+ * forward's stream, with no synchronisation, tagged QW_SPAN_*: the first
+ * LN-mod, the QKV linear (with its q/k norm + RoPE, and its int8 widening
+ * pass where it has one), attention, the out linear + gate, the second
+ * LN-mod, the up linear (+ GELU or SwiGLU), the down linear + gate. The
+ * caller reads them with qw_gpu_span_collect (at most 4096 between
+ * collects: 18 forwards of 32 layers). */
+enum { QW_SPAN_LN1 = 0, QW_SPAN_QKV, QW_SPAN_ATTN, QW_SPAN_OUT, QW_SPAN_LN2, QW_SPAN_UP,
+       QW_SPAN_DOWN, QW_SPAN_COUNT };
+int qw_dit_set_spans(qw_dit *dit, int on);
+
 /* Diagnostic trace of the t2i forward (qw_dit_forward*), for per-block
  * parity checks; no reference counterpart (the reference dumps stages
  * through its QWEN_* diagnostic switches instead). While set, each

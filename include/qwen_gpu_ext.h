@@ -143,6 +143,16 @@ int qw_gpu_linear(h3_gpu *gpu, const qw_linear_desc *desc);
  * contents. */
 int qw_gpu_linear_static(h3_gpu *gpu, const qw_linear_desc *desc);
 
+/* No counterpart in the reference (a measurement aid, like h3_gpu_timer_*):
+ * spans time pieces of the work on the stream without synchronising it.
+ * span_begin records an event tagged `tag`, span_end the matching end
+ * event; spans do not nest. span_collect waits for the last span, writes
+ * up to max (tag, device ms) pairs, forgets all spans and returns how many
+ * it wrote, or -1 on error. At most 4096 spans between collects. */
+int qw_gpu_span_begin(h3_gpu *gpu, int tag);
+int qw_gpu_span_end(h3_gpu *gpu);
+int qw_gpu_span_collect(h3_gpu *gpu, int *tags, double *ms, int max);
+
 /* Fused per-head RMSNorm (single rounding, h3_shaders.metal:4309-4329) and
  * interleaved RoPE (h3_shaders.metal:4864-4896) over q and k in one
  * strided buffer [rows, ld]: q heads at column 0, k heads at k_offset.

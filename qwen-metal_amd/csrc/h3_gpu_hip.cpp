@@ -50,6 +50,8 @@ static const char *k_names[K_COUNT] = {
  * W8 force one route wherever it can run. */
 enum { QW_INT8_AUTO = 0, QW_INT8_WIDEN = 1, QW_INT8_W8 = 2 };
 
+#define QW_SPAN_MAX 4096
+
 struct h3_gpu {
     int device;
     hipStream_t stream;
@@ -65,6 +67,10 @@ struct h3_gpu {
     size_t scratch_bytes;
     uint32_t attn_threads; /* attention workgroup size, 64 per 32-query wave */
     int int8_route; /* QW_INT8_* : how int8 linears of many rows run */
+    /* qw_gpu_span_*: event pairs recorded on the stream, read after a sync */
+    hipEvent_t *span_ev;
+    int *span_tag;
+    int span_n, span_open;
     void *widen; /* bf16 copy of the int8 weight of the linear in flight */
     size_t widen_bytes;
     uint32_t cus;      /* compute units */
@@ -164,6 +170,10 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     g->scratch_bytes = 0;
     g->widen = NULL;
     g->widen_bytes = 0;
+    g->span_ev = NULL;
+    g->span_tag = NULL;
+    g->span_n = 0;
+    g->span_open = 0;
     g->int8_route = QW_INT8_AUTO;
     if (const char *r = getenv("QW_INT8_ROUTE")) {
         if (!strcmp(r, "w8")) g->int8_route = QW_INT8_W8;
@@ -240,6 +250,11 @@ extern "C" void h3_gpu_free(h3_gpu *g) {
     if (g->widen) hipFree(g->widen);
     if (g->sk_part) hipFree(g->sk_part);
     if (g->sk_flag) hipFree(g->sk_flag);
+    if (g->span_ev) {
+        for (int i = 0; i < 2 * QW_SPAN_MAX; i++) hipEventDestroy(g->span_ev[i]);
+        free(g->span_ev);
+        free(g->span_tag);
+    }
     hipEventDestroy(g->timer0);
     hipEventDestroy(g->timer1);
     hipEventDestroy(g->chain0);
@@ -314,6 +329,69 @@ extern "C" double h3_gpu_timer_end(h3_gpu *g) {
     float ms = 0;
     if (hipEventElapsedTime(&ms, g->timer0, g->timer1) != hipSuccess) return -1.0;
     return ms;
+}
+
+/* Spans: a begin and an end event recorded on the stream around a piece of
+ * work, no synchronisation; qw_gpu_span_collect waits for the last one and
+ * returns every span's device time. Up to QW_SPAN_MAX spans between
+ * collects; events are created on the first span. */
+extern "C" int qw_gpu_span_begin(h3_gpu *g, int tag) {
+    if (!g) return 0;
+    if (g->span_open) return fail(g, "span_begin: a span is already open");
+    if (!g->span_ev) {
+        g->span_ev = (hipEvent_t *)calloc(2 * QW_SPAN_MAX, sizeof(hipEvent_t));
+        g->span_tag = (int *)calloc(QW_SPAN_MAX, sizeof(int));
+        if (!g->span_ev || !g->span_tag) return fail(g, "span_begin: out of host memory");
+        for (int i = 0; i < 2 * QW_SPAN_MAX; i++)
+            if (hipEventCreate(&g->span_ev[i]) != hipSuccess) {
+                for (int j = 0; j < i; j++) hipEventDestroy(g->span_ev[j]);
+                free(g->span_ev);
+                free(g->span_tag);
+                g->span_ev = NULL;
+                g->span_tag = NULL;
+                return fail(g, "span_begin: event creation failed");
+            }
+    }
+    if (g->span_n >= QW_SPAN_MAX) return fail(g, "span_begin: more than %d spans", QW_SPAN_MAX);
+    g->span_tag[g->span_n] = tag;
+    if (hipEventRecord(g->span_ev[2 * g->span_n], g->stream) != hipSuccess)
+        return fail(g, "span_begin: event record failed");
+    g->span_open = 1;
+    return 1;
+}
+
+extern "C" int qw_gpu_span_end(h3_gpu *g) {
+    if (!g) return 0;
+    if (!g->span_open) return fail(g, "span_end: no open span");
+    if (hipEventRecord(g->span_ev[2 * g->span_n + 1], g->stream) != hipSuccess)
+        return fail(g, "span_end: event record failed");
+    g->span_open = 0;
+    g->span_n++;
+    return 1;
+}
+
+extern "C" int qw_gpu_span_collect(h3_gpu *g, int *tags, double *ms, int max) {
+    if (!g) return -1;
+    if (g->span_open) {
+        fail(g, "span_collect: a span is still open");
+        return -1;
+    }
+    const int n = g->span_n < max ? g->span_n : max;
+    if (g->span_n && hipEventSynchronize(g->span_ev[2 * g->span_n - 1]) != hipSuccess) {
+        fail(g, "span_collect: event wait failed");
+        return -1;
+    }
+    for (int i = 0; i < n; i++) {
+        float t = 0;
+        if (hipEventElapsedTime(&t, g->span_ev[2 * i], g->span_ev[2 * i + 1]) != hipSuccess) {
+            fail(g, "span_collect: elapsed time unavailable");
+            return -1;
+        }
+        if (tags) tags[i] = g->span_tag[i];
+        if (ms) ms[i] = t;
+    }
+    g->span_n = 0;
+    return n;
 }
 
 /* ---------------------------------------------------------------------- */

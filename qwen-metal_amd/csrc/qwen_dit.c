@@ -62,6 +62,7 @@ struct qw_dit {
     uint32_t rm_rows, rm_text, rm_batch;
     int profile;
     double prof_ms[P_COUNT];
+    int spans; /* qw_dit_set_spans: stage spans on the stream (QW_SPAN_*) */
     /* qw_dit_set_trace: per-block hidden states and the modulation */
     h3_gpu_tensor *trace_hidden, *trace_mod;
     /* LoRA adapters, in stack order; while any is active, base[4 l + j]
@@ -888,6 +889,20 @@ static void prof_end(qw_dit *d, int stage) {
     }
 }
 
+static void span_b(qw_dit *d, int tag) {
+    if (d->spans) qw_gpu_span_begin(d->gpu, tag);
+}
+
+static void span_e(qw_dit *d) {
+    if (d->spans) qw_gpu_span_end(d->gpu);
+}
+
+int qw_dit_set_spans(qw_dit *d, int on) {
+    if (!d) return 0;
+    d->spans = on != 0;
+    return 1;
+}
+
 int qw_dit_block_profile(const qw_dit *d, double *ms, int max_stages) {
     if (!d || !ms) return 0;
     int n = max_stages < P_COUNT ? max_stages : P_COUNT;
@@ -1031,9 +1046,13 @@ static int block_run(qw_dit *d, int li, h3_gpu_tensor *hidden, uint32_t batch, u
     int ok;
 
     prof_begin(d);
+    span_b(d, QW_SPAN_LN1);
     ok = qw_gpu_layer_norm_mod_shift_bf16(g, d->ws_mod, hidden, modulation, row_map, M, H, S, 0,
-                                          sh ? 4 : -1, 1e-6f) &&
-         qkv_linear(d, L, M, rope_cos, rope_sin, rows);
+                                          sh ? 4 : -1, 1e-6f);
+    span_e(d);
+    span_b(d, QW_SPAN_QKV);
+    ok = ok && qkv_linear(d, L, M, rope_cos, rope_sin, rows);
+    span_e(d);
     prof_end(d, P_INPUT);
     if (!ok) return 0;
 
@@ -1067,7 +1086,9 @@ static int block_run(qw_dit *d, int li, h3_gpu_tensor *hidden, uint32_t batch, u
         ad.kv_limit = NULL;
         ad.text_rows = 0; /* every query sees every cached key */
     }
+    span_b(d, QW_SPAN_ATTN);
     ok = qw_gpu_attention_bf16(g, &ad);
+    span_e(d);
     if (ok && k_out) ok = qw_gpu_copy_rows(g, k_out, 0, H, d->ws_qkv, H, 3 * H, M, H);
     if (ok && v_out) ok = qw_gpu_copy_rows(g, v_out, 0, H, d->ws_qkv, 2 * (size_t)H, 3 * H, M, H);
     if (ok && debug_attn) ok = h3_gpu_copy_bf16(g, debug_attn, 0, d->ws_attn, 0, (size_t)M * H);
@@ -1075,27 +1096,39 @@ static int block_run(qw_dit *d, int li, h3_gpu_tensor *hidden, uint32_t batch, u
     if (!ok) return 0;
 
     prof_begin(d);
+    span_b(d, QW_SPAN_OUT);
     ok = linear(d, &L->out, hidden, 0, H, d->ws_attn, 0, H, M, QW_LINEAR_GATE, modulation, row_map,
                 S, 2);
+    span_e(d);
     prof_end(d, P_OUT);
     if (!ok) return 0;
 
     prof_begin(d);
+    span_b(d, QW_SPAN_LN2);
     ok = qw_gpu_layer_norm_mod_shift_bf16(g, d->ws_mod, hidden, modulation, row_map, M, H, S, 1,
                                           sh ? 5 : -1, 1e-6f);
+    span_e(d);
     prof_end(d, P_LN);
     if (!ok) return 0;
 
     prof_begin(d);
     if (d->cfg.mlp_act == QW_MLP_GELU_TANH) {
-        ok = plain(d, &L->fc1, d->ws_wide, d->ws_mod, M, QW_LINEAR_GELU) &&
-             linear(d, &L->fc2, hidden, 0, H, d->ws_wide, 0, F, M, QW_LINEAR_GATE, modulation,
-                    row_map, S, 3);
+        span_b(d, QW_SPAN_UP);
+        ok = plain(d, &L->fc1, d->ws_wide, d->ws_mod, M, QW_LINEAR_GELU);
+        span_e(d);
+        span_b(d, QW_SPAN_DOWN);
+        ok = ok && linear(d, &L->fc2, hidden, 0, H, d->ws_wide, 0, F, M, QW_LINEAR_GATE,
+                          modulation, row_map, S, 3);
+        span_e(d);
     } else {
+        span_b(d, QW_SPAN_UP);
         ok = plain(d, &L->fc1, d->ws_wide, d->ws_mod, M, QW_LINEAR_STORE) &&
-             qw_gpu_swiglu_bf16(g, d->ws_act, d->ws_wide, M, F) &&
-             linear(d, &L->fc2, hidden, 0, H, d->ws_act, 0, F, M, QW_LINEAR_GATE, modulation,
-                    row_map, S, 3);
+             qw_gpu_swiglu_bf16(g, d->ws_act, d->ws_wide, M, F);
+        span_e(d);
+        span_b(d, QW_SPAN_DOWN);
+        ok = ok && linear(d, &L->fc2, hidden, 0, H, d->ws_act, 0, F, M, QW_LINEAR_GATE,
+                          modulation, row_map, S, 3);
+        span_e(d);
     }
     prof_end(d, P_MLP);
     return ok;

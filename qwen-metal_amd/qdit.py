@@ -193,6 +193,10 @@ SIGNATURES = {
     "qw_pipe_rope_tables": (C.c_int, [vp, u32, u32, u32, vp, vp, C.c_char_p, sz]),
     "qw_pipe_rope_tables_host": (None, [u32, u32, u32, vp, vp]),
     "qw_pipe_rope_tables_blocks": (C.c_int, [vp, vp, vp, vp, u32, vp, vp, C.c_char_p, sz]),
+    "qw_gpu_span_begin": (C.c_int, [vp, C.c_int]),
+    "qw_gpu_span_end": (C.c_int, [vp]),
+    "qw_gpu_span_collect": (C.c_int, [vp, vp, vp, C.c_int]),
+    "qw_dit_set_spans": (C.c_int, [vp, C.c_int]),
     "qw_pipe_rope_tables_blocks_host": (sz, [vp, vp, vp, u32, vp, vp]),
     "h3_st_read_header": (C.c_int, [C.c_char_p, vp, C.c_char_p, sz]),
     "h3_st_free_header": (None, [vp]),

@@ -667,3 +667,47 @@ def test_lora_fusion_stack(gpu, qd, oracle, tmp_path):
     err = C.create_string_buffer(512)
     assert not L.qw_dit_apply_lora(q8.h, p1, 1.0, err, 512) and b"int8" in err.value
     q8.close()
+
+
+def test_stage_spans(gpu, qd, oracle):
+    """qw_dit_set_spans: one forward records one span per stage per block
+    (QW_SPAN_* order: LN-mod, QKV, attention, out, LN-mod, up, down), each
+    a positive device time, with no synchronisation inside the forward;
+    the output is the same as without spans. Misuse is an error, not a
+    hang: a second begin while one is open, a collect with one open."""
+    import ctypes as C
+    L = qd.lib()
+    c = cfg("small", **BASE_VARIANT)
+    T, gh, gw, B = 16, 8, 8, 2
+    I, R = gh * gw, T + gh * gw
+    text = oracle.fill_normal_bf16(B * T * c["text_dim"], 5, 970)
+    lat = oracle.fill_normal_bf16(B * I * c["z_dim"], 5, 971)
+    cos, sin = oracle.rope_tables(T, gh, gw)
+    ins = [gpu.put(text), gpu.put(lat), gpu.put(cos), gpu.put(sin)]
+    dit = qd.Dit(gpu, c, 5)
+    outs = []
+    tags = (C.c_int * 4096)()
+    ms = (C.c_double * 4096)()
+    for on in (0, 1):
+        assert L.qw_dit_set_spans(dit.h, on)
+        out = gpu.new(B * R * c["z_dim"], qd.BF16)
+        dit.forward_batch(ins[0], T, ins[1], I, B, 0.6, ins[2], ins[3], out)
+        n = L.qw_gpu_span_collect(gpu.h, tags, ms, 4096)
+        gpu.submit()
+        outs.append(out.read())
+        if on:
+            assert n == 7 * c["layers"]
+            assert list(tags[:n]) == list(range(7)) * c["layers"]
+            assert all(ms[i] > 0 for i in range(n))
+        else:
+            assert n == 0
+    assert L.qw_dit_set_spans(dit.h, 0)
+    dit.close()
+    assert np.array_equal(outs[0], outs[1])
+    assert L.qw_gpu_span_begin(gpu.h, 0) == 1
+    assert L.qw_gpu_span_begin(gpu.h, 1) == 0
+    assert L.qw_gpu_span_collect(gpu.h, tags, ms, 4096) == -1
+    assert L.qw_gpu_span_end(gpu.h) == 1
+    assert L.qw_gpu_span_end(gpu.h) == 0
+    assert L.qw_gpu_span_collect(gpu.h, tags, ms, 4096) == 1
+    gpu.submit()
