@@ -248,12 +248,14 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
         }
     };
     /* S^T of one tile: keys kv0 + 32 kbk + [0, 32), one MFMA per 16-d step;
-     * steps [i0, i1) of the 8 AKB (kbk, st) pairs, kbk-major */
+     * steps [i0, i1) of the 8 AKB (kbk, st) pairs, st-major, so consecutive
+     * MFMAs go to the AKB independent accumulators (measured 1% faster than
+     * running each accumulator's 8 dependent MFMAs back to back) */
     auto qk = [&](uint32_t kstage, floatx16 (&s)[AKB], int i0, int i1) __attribute__((always_inline)) {
         const unsigned char *ks = lds + kstage * A_TILE;
 #pragma unroll
         for (int i = i0; i < i1; i++) {
-            const int kbk = i / 8, st = i % 8;
+            const int kbk = i % AKB, st = i / AKB;
             if (st == 0) {
 #pragma unroll
                 for (int v = 0; v < 16; v++) s[kbk][v] = 0.0f;
@@ -271,19 +273,27 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
      * (rows 16 tk + 4 h + 0..3, then 16 tk + 8 + 4 h + 0..3). */
     const uint32_t tq = lane & 3, te = (lane >> 2) & 3;
     const uint32_t tdb = 16 * ((lane >> 4) & 1) + 4 * tq; /* d offset inside a 32-d block */
-    auto pv = [&](uint32_t vstage, const bf16x8 (&pf)[2 * AKB]) __attribute__((always_inline)) {
+    auto read_v = [&](uint32_t vstage, int tk, int db) __attribute__((always_inline)) {
         const unsigned char *vs = lds + (2 + vstage) * A_TILE;
+        const uint32_t d = 32 * db + tdb, cc = d >> 3, half = (d >> 2) & 1;
+        const uint32_t r0 = 16 * tk + 4 * h + te, r1 = r0 + 8;
+        const bf16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (attn_lds_b4 *)(vs + r0 * 256 + ((cc ^ (4 * (r0 & 3))) << 4) + half * 8));
+        const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+            (attn_lds_b4 *)(vs + r1 * 256 + ((cc ^ (4 * (r1 & 3))) << 4) + half * 8));
+        return bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+    };
+    /* vpre: the V^T fragments of the first VPRE 16-key steps, read at the
+     * top of the tile (V(t) landed at the previous barrier) so the first P.V
+     * MFMAs do not wait on LDS */
+    constexpr int VPRE = 2;
+    auto pv = [&](uint32_t vstage, const bf16x8 (&pf)[2 * AKB], const bf16x8 (&vpre)[VPRE][4])
+        __attribute__((always_inline)) {
 #pragma unroll
         for (int tk = 0; tk < 2 * AKB; tk++) {
 #pragma unroll
             for (int db = 0; db < 4; db++) {
-                const uint32_t d = 32 * db + tdb, cc = d >> 3, half = (d >> 2) & 1;
-                const uint32_t r0 = 16 * tk + 4 * h + te, r1 = r0 + 8;
-                const bf16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                    (attn_lds_b4 *)(vs + r0 * 256 + ((cc ^ (4 * (r0 & 3))) << 4) + half * 8));
-                const bf16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                    (attn_lds_b4 *)(vs + r1 * 256 + ((cc ^ (4 * (r1 & 3))) << 4) + half * 8));
-                const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                const bf16x8 vf = tk < VPRE ? vpre[tk < VPRE ? tk : 0][db] : read_v(vstage, tk, db);
                 o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[tk], o[db], 0, 0, 0);
             }
         }
@@ -362,9 +372,14 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
         constexpr uint32_t st = decltype(odd)::value; /* t & 1, known at compile time */
         const uint32_t kv0 = t * AKT;
         issue(st, kv0 + 2 * AKT, st ^ 1, kv0 + AKT);
+        bf16x8 vpre[VPRE][4];
+#pragma unroll
+        for (int tk = 0; tk < VPRE; tk++)
+#pragma unroll
+            for (int db = 0; db < 4; db++) vpre[tk][db] = read_v(st, tk, db);
         bf16x8 pf[2 * AKB];
         softmax_qk(sc, pf, kv0, st ^ 1, sn);
-        pv(st, pf);
+        pv(st, pf, vpre);
         __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): K(t + 2), V(t + 1) landed */
         attn_barrier();
     };
