@@ -9,9 +9,9 @@
  * Scores are computed transposed, S^T = K Q^T, with
  * v_mfma_f32_32x32x16_bf16: in that output layout each lane holds ONE query
  * (column lane % 32) and 16 keys per 32-key block, so the row max / row sum
- * of the online softmax need one cross-half exchange (lane ^ 32) instead of
- * a 32-lane reduction, and the per-query rescale of the output is a lane
- * scalar. The output is accumulated transposed too, O^T = V^T P^T: the
+ * of the online softmax need at most one cross-half exchange (lane ^ 32)
+ * instead of a 32-lane reduction (the max only when it moves, the sum once
+ * at the end), and the per-query rescale of the output is a lane scalar. The output is accumulated transposed too, O^T = V^T P^T: the
  * probabilities stay in registers and feed the MFMA B operand directly.
  * Within each 16-key K-step the keys are permuted identically in the V^T
  * (A) and P^T (B) operands, which leaves the contraction unchanged.
@@ -299,7 +299,7 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
         }
     };
 
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f; /* l_run: this lane's half of the keys */
     /* Online-softmax step of a tile whose S is in `sc`, with the QK MFMAs of
      * the next tile (into `sn`) laid out between its VALU work. The running
      * max moves lazily: only when a row's tile max exceeds it by more than
@@ -319,7 +319,6 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
         for (int kbk = 0; kbk < AKB; kbk++)
 #pragma unroll
             for (int v = 0; v < 16; v++) mt = fmaxf(mt, sc[kbk][v]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
         for (int i = 0; i < QK_PRE; i++) {
@@ -327,9 +326,12 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
             __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
             if (i + 2 < QK_PRE) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        const float m_new = mt * c;
-        const bool move = m_new > m_run + 8.0f;
-        if (__builtin_amdgcn_ballot_w64(move)) {
+        /* mt is this lane's half of the query's keys; the query's max
+         * exceeds m_run + 8 exactly when one of its halves does, so the
+         * cross-half exchange runs only on the (rare) move path */
+        if (__builtin_amdgcn_ballot_w64(mt * c > m_run + 8.0f)) {
+            const float m_new = fmaxf(mt, __shfl_xor(mt, 32, 64)) * c;
+            const bool move = m_new > m_run + 8.0f;
             const float m_to = move ? m_new : m_run;
             const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_to);
             l_run *= alpha;
@@ -350,8 +352,7 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
             __builtin_amdgcn_sched_group_barrier(0x002, QK_NV, 0);
             if (i + 2 < 8 * AKB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
-        rs += __shfl_xor(rs, 32, 64);
-        l_run += rs;
+        l_run += rs; /* this half's keys; the halves are added at the end */
     };
 
     /* prologue: K(0), V(0), K(1) staged; S(0) computed */
@@ -391,5 +392,5 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
     if (t < ntiles) iter(s0, s1, t, std::integral_constant<uint32_t, 0>());
 
     /* ---- normalise and store: o[db][v] = O[r][32 db + 8 (v/4) + 4 h + v%4] */
-    attn_store_rows(a, o, l_run, b, r, head, h);
+    attn_store_rows(a, o, l_run + __shfl_xor(l_run, 32, 64), b, r, head, h);
 }
