@@ -381,6 +381,19 @@ def cpu_baseline(runs=5):
             "configs": res}
 
 
+def calibration_copy(qd, gpu):
+    """The counter calibration of the profile modes: a plain copy
+    (qw_copy2d) of 256 MiB, launched three times."""
+    copy_elems = 128 << 20  # bf16: 256 MiB
+    src, dst = gpu.new(copy_elems, qd.BF16), gpu.new(copy_elems, qd.BF16)
+    for _ in range(3):
+        gpu.check(qd.lib().qw_gpu_copy_rows(gpu.h, dst.h, 0, 4096, src.h, 0, 4096,
+                                            copy_elems // 4096, 4096), "copy")
+    gpu.submit()
+    src.free()
+    dst.free()
+
+
 def profile_kernel(qd, gpu, reps=5):
     """Launch-only mode for rocprofv3 --pmc passes: a plain copy of a known
     size (the counter calibration: 256 MiB read + 256 MiB written), then
@@ -389,11 +402,7 @@ def profile_kernel(qd, gpu, reps=5):
     epilogue -- `reps` times. Nothing is timed or printed as a result."""
     H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
     L = qd.lib()
-    copy_elems = 128 << 20  # bf16: 256 MiB
-    src, dst = gpu.new(copy_elems, qd.BF16), gpu.new(copy_elems, qd.BF16)
-    for _ in range(3):
-        gpu.check(L.qw_gpu_copy_rows(gpu.h, dst.h, 0, 4096, src.h, 0, 4096,
-                                     copy_elems // 4096, 4096), "copy")
+    calibration_copy(qd, gpu)
     a = gpu.new(M * F, qd.BF16)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, a.h, 0, M * F, 1, 1, 1.0, 0.0), "fill")
     wb, q, s = gpu.new(F * H, qd.BF16), gpu.new(F * H, qd.I8), gpu.new(H, qd.F32)
@@ -408,11 +417,12 @@ def profile_kernel(qd, gpu, reps=5):
 
 
 def profile_attention(qd, gpu, reps=5):
-    """Launch-only mode for rocprofv3 --pmc: the step's attention call
-    (batch 2 x 24 heads x 4352 rows over the fused q|k|v buffer, text rows
-    attending the text prefix) `reps` times."""
+    """Launch-only mode for rocprofv3 --pmc: the calibration copy, then the
+    step's attention call (batch 2 x 24 heads x 4352 rows over the fused
+    q|k|v buffer, text rows attending the text prefix) `reps` times."""
     H, M, R = CFG["hidden"], BATCH * (TEXT + GH * GW), TEXT + GH * GW
     L = qd.lib()
+    calibration_copy(qd, gpu)
     qkv = gpu.new(M * 3 * H, qd.BF16)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, qkv.h, 0, M * 3 * H, 1, 3, 1.0, 0.0), "fill")
     att = gpu.new(M * H, qd.BF16)
