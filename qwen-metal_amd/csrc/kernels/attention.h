@@ -285,9 +285,10 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
     };
     /* vpre: the V^T fragments of the first VPRE 16-key steps, read at the
      * top of the tile (V(t) landed at the previous barrier) so the first P.V
-     * MFMAs do not wait on LDS */
-    constexpr int VPRE = 2;
-    auto pv = [&](uint32_t vstage, const bf16x8 (&pf)[2 * AKB], const bf16x8 (&vpre)[VPRE][4])
+     * MFMAs do not wait on LDS (one step: two would spill beside the scores
+     * the softmax keeps for its rare path) */
+    constexpr int VPRE = 1;
+    auto pv = [&](uint32_t vstage, const bf16x8 (&pf)[2 * AKB], const bf16x8 (&vpre)[VPRE > 0 ? VPRE : 1][4])
         __attribute__((always_inline)) {
 #pragma unroll
         for (int tk = 0; tk < 2 * AKB; tk++) {
@@ -301,56 +302,56 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
 
     float m_run = -INFINITY, l_run = 0.0f; /* l_run: this lane's half of the keys */
     /* Online-softmax step of a tile whose S is in `sc`, with the QK MFMAs of
-     * the next tile (into `sn`) laid out between its VALU work. The running
-     * max moves lazily: only when a row's tile max exceeds it by more than
-     * 2^8, or on the first finite max, so p <= 256; a move rescales O and l
-     * first (a rare, wave-uniform branch). Then P = bf16(exp2(S c - m)) and
-     * the row sum, once. */
-    /* QK MFMAs issued under the tile max, VALU instructions placed after
-     * each later QK MFMA (measured: 8 and 4 beat 2, 4 and 3, 6, 8) */
-    constexpr int QK_PRE = 8, QK_NV = 4;
+     * the next tile (into `sn`) laid out between its VALU work: P =
+     * bf16(exp2(S c - m)) and the row sum. The running max m moves lazily:
+     * only when a row's tile max exceeds it by more than 8 (log2 units), or
+     * on the first finite max, so p <= 2^8; a move rescales O and l and
+     * recomputes P (a rare, wave-uniform branch). */
+    /* VALU instructions placed after each QK MFMA (measured: 2 ahead of 1,
+     * 3, 4, 5, 6, 8, 10 and of no placement hints, by 0.5-2%) */
+    constexpr int QK_NV = 2;
     auto softmax_qk = [&](floatx16 (&sc)[AKB], bf16x8 (&pf)[2 * AKB], uint32_t kv0,
                           uint32_t kstage_next, floatx16 (&sn)[AKB]) __attribute__((always_inline)) {
         if (kv0 + AKT > lmin) attn_mask(sc, kv0, L, h);
-        /* the first QK MFMAs of the next tile run under the tile max */
-        qk(kstage_next, sn, 0, QK_PRE);
-        float mt = -INFINITY;
-#pragma unroll
-        for (int kbk = 0; kbk < AKB; kbk++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) mt = fmaxf(mt, sc[kbk][v]);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-        for (int i = 0; i < QK_PRE; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-            if (i + 2 < QK_PRE) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        /* mt is this lane's half of the query's keys; the query's max
-         * exceeds m_run + 8 exactly when one of its halves does, so the
-         * cross-half exchange runs only on the (rare) move path */
-        if (__builtin_amdgcn_ballot_w64(mt * c > m_run + 8.0f)) {
-            const float m_new = fmaxf(mt, __shfl_xor(mt, 32, 64)) * c;
-            const bool move = m_new > m_run + 8.0f;
-            const float m_to = move ? m_new : m_run;
-            const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_to);
-            l_run *= alpha;
-#pragma unroll
-            for (int db = 0; db < 4; db++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) o[db][v] *= alpha;
-            m_run = m_to;
-        }
+        /* P with the running max as it stands; the QK MFMAs of the next tile
+         * are laid out between the exp, convert and sum VALU instructions,
+         * their K fragment reads two MFMAs ahead */
         float rs = attn_exp(sc, pf, c, m_run == -INFINITY ? 0.0f : m_run);
-        qk(kstage_next, sn, QK_PRE, 8 * AKB);
-        /* K fragment reads run two MFMAs ahead; the exp, convert and sum
-         * VALU fills the issue slots between MFMAs */
+        qk(kstage_next, sn, 0, 8 * AKB);
         __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
-        for (int i = QK_PRE; i < 8 * AKB; i++) {
+        for (int i = 0; i < 8 * AKB; i++) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x002, QK_NV, 0);
             if (i + 2 < 8 * AKB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        /* The running max moves when the tile max exceeds it by more than 8
+         * (log2 units), i.e. when some p would exceed 2^8; every p is at most
+         * this half's sum of the rounded p, so a half whose sum stays below
+         * 256 needs no move. Only otherwise (and while the max is still
+         * -inf) is the tile max computed and the rule applied, with P
+         * recomputed after a move: the same P, l and O as applying the rule
+         * on every tile. */
+        if (__builtin_amdgcn_ballot_w64(rs >= 256.0f || m_run == -INFINITY)) {
+            float mt = -INFINITY;
+#pragma unroll
+            for (int kbk = 0; kbk < AKB; kbk++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) mt = fmaxf(mt, sc[kbk][v]);
+            const float m_new = fmaxf(mt, __shfl_xor(mt, 32, 64)) * c;
+            const bool move = m_new > m_run + 8.0f;
+            if (__builtin_amdgcn_ballot_w64(move)) {
+                const float m_to = move ? m_new : m_run;
+                const float alpha =
+                    m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_to);
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < 4; db++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) o[db][v] *= alpha;
+                m_run = m_to;
+                rs = attn_exp(sc, pf, c, m_run == -INFINITY ? 0.0f : m_run);
+            }
         }
         l_run += rs; /* this half's keys; the halves are added at the end */
     };
@@ -373,7 +374,7 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
         constexpr uint32_t st = decltype(odd)::value; /* t & 1, known at compile time */
         const uint32_t kv0 = t * AKT;
         issue(st, kv0 + 2 * AKT, st ^ 1, kv0 + AKT);
-        bf16x8 vpre[VPRE][4];
+        bf16x8 vpre[VPRE > 0 ? VPRE : 1][4];
 #pragma unroll
         for (int tk = 0; tk < VPRE; tk++)
 #pragma unroll
