@@ -330,8 +330,8 @@ __device__ __forceinline__ void gemm_epilogue_mode(const qw_gemm_args &a, SlabWr
             for (int i = 0; i < RP; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    float t0 = y[i][2 * j], t1 = y[i][2 * j + 1];
-                    if (scaled) t0 *= sc[2 * j], t1 *= sc[2 * j + 1];
+                    /* sc is 1 where there is no scale: the product is exact */
+                    const float t0 = y[i][2 * j] * sc[2 * j], t1 = y[i][2 * j + 1] * sc[2 * j + 1];
                     pk[i][j] = pack_bf(t0 + bias[2 * j], t1 + bias[2 * j + 1]);
                     y[i][2 * j] = lo_bf(pk[i][j]);
                     y[i][2 * j + 1] = hi_bf(pk[i][j]);

@@ -606,7 +606,10 @@ __device__ __forceinline__ void qg_finish_at(const qw_gemm_args &a, unsigned cha
     float *region = (float *)((wave < 2 ? lds : lds_b) + (wave & 1) * REG);
     const uint32_t poff = wm * 128 * 256 + wn * 128;
     /* slab mi: rows 32 mi + 16 q + lane % 16 (tile mb = 2 mi + q), columns
-     * 32 ni + 16 p + 4 (lane / 16) + 0..3 (tile nb = 2 ni + p) */
+     * 32 ni + 16 p + 4 (lane / 16) + 0..3 (tile nb = 2 ni + p). Columns
+     * 64-127 are stored with the two 16-byte halves of each 32-byte group
+     * exchanged (column c at c ^ 4). */
+    const uint32_t wc_lo = 4 * (lane >> 4), wc_hi = wc_lo ^ 4; /* column within 16, plain / exchanged */
     auto write_slab = [&](int mi) __attribute__((always_inline)) {
 #pragma unroll
         for (int ni = 0; ni < 4; ni++)
@@ -615,19 +618,20 @@ __device__ __forceinline__ void qg_finish_at(const qw_gemm_args &a, unsigned cha
 #pragma unroll
                 for (int q = 0; q < 2; q++)
                     *(floatx4 *)(region + (16 * q + (lane & 15)) * LDF + ni * 32 + 16 * p +
-                                 4 * (lane >> 4)) = acc[2 * mi + q][2 * ni + p];
+                                 (ni >= 2 ? wc_hi : wc_lo)) = acc[2 * mi + q][2 * ni + p];
     };
-    /* first/second 16-byte halves of the lane's 32 read-back bytes:
-     * lanes 8-15 of a row start with the upper half, so one ds_read_b128
-     * pass covers all 64 banks */
+    /* the lane's 32 read-back bytes (columns 8 cc..8 cc + 7) as two
+     * ds_read_b128: lanes 8-15 of a row (columns 64-127, stored exchanged)
+     * read the upper physical half first, so one pass of 16 lanes covers all
+     * 64 banks and both reads return the columns in order */
     const uint32_t cc = lane & 15, swap = (cc >> 3) & 1;
     auto read_row = [&](uint32_t lr, float (&v)[8]) __attribute__((always_inline)) {
         const floatx4 v0 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * swap);
         const floatx4 v1 = *(const floatx4 *)(region + lr * LDF + cc * 8 + 4 * (swap ^ 1));
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            v[j] = swap ? v1[j] : v0[j];
-            v[4 + j] = swap ? v0[j] : v1[j];
+            v[j] = v0[j];
+            v[4 + j] = v1[j];
         }
     };
     gemm_epilogue_lds<EPI, INT8, MB / 2, 32, 8>(a, write_slab, read_row, row0, col0, lane,
