@@ -1001,6 +1001,18 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     } else if (d->epilogue != QW_LINEAR_STORE && d->epilogue != QW_LINEAR_GELU) {
         return fail(g, "linear: unknown epilogue %d", d->epilogue);
     }
+    if (d->epilogue == QW_LINEAR_QKNORM && d->rope_rows < 128) {
+        /* the fused epilogue wraps a 128-row block's RoPE table rows with one
+         * subtraction, which needs a table of at least 128 rows; a shorter
+         * one runs the plain linear, then the standalone norm + RoPE
+         * (bit-identical to the fused epilogue) */
+        qw_linear_desc plain = *d;
+        plain.epilogue = QW_LINEAR_STORE;
+        if (!linear_impl(g, &plain, no_alloc)) return 0;
+        return qw_gpu_qk_norm_rope_bf16(g, d->out, d->rows, d->cols / 384, d->ldc, d->cols / 3,
+                                        d->norm_q, d->norm_k, d->rope_cos, d->rope_sin,
+                                        d->rope_rows, d->eps);
+    }
     /* at most 8 rows, plain or GELU epilogue: one wave per 2 output columns
      * streams the weight once */
     if (d->rows <= 8 &&

@@ -245,6 +245,16 @@ __device__ __forceinline__ void gemm_epilogue_mode(const qw_gemm_args &a, SlabWr
 #pragma unroll
         for (int i = 0; i < 4; i++) nw[2 * i] = lo_bf(wn[i]), nw[2 * i + 1] = hi_bf(wn[i]);
     }
+    /* RoPE table row (row % rope_rows) of this lane's row row0 + rr + off,
+     * from one division per tile: the rows are consecutive and off < 128,
+     * and the host sends only tables of at least 128 rows here, so one
+     * subtraction wraps each. Rows past the output read a row of the table
+     * and are not stored. */
+    const uint32_t rope_base = EPI == QW_EPI_QKNORM && qk_head ? (row0 + rr) % a.rope_rows : 0;
+    auto rope_row = [&](uint32_t off) __attribute__((always_inline)) {
+        const uint32_t r = rope_base + off;
+        return r >= a.rope_rows ? r - a.rope_rows : r;
+    };
 #pragma unroll
     for (int mi = 0; mi < NSLAB; mi++) {
         write_slab(mi); /* fp32 sums of rows [SR mi, SR mi + SR) into the LDS region */
@@ -267,8 +277,7 @@ __device__ __forceinline__ void gemm_epilogue_mode(const qw_gemm_args &a, SlabWr
             if (EPI == QW_EPI_QKNORM && qk_head) {
 #pragma unroll
                 for (int i = 0; i < RP; i++) {
-                    const uint32_t row = min(row0 + mi * SR + 4 * (p0 + i) + rr, a.m - 1);
-                    const size_t t = (size_t)(row % a.rope_rows) * 64 + 4 * cc;
+                    const size_t t = (size_t)rope_row(mi * SR + 4 * (p0 + i)) * 64 + 4 * cc;
                     rc[i] = *(const floatx4 *)(a.rope_cos + t);
                     rs[i] = *(const floatx4 *)(a.rope_sin + t);
                 }
@@ -353,7 +362,12 @@ __device__ __forceinline__ void gemm_epilogue_mode(const qw_gemm_args &a, SlabWr
                 for (int i = 0; i < RP; i++) {
                     const float inv = head_rms_inv(ss[i], a.eps);
 #pragma unroll
-                    for (int j = 0; j < 8; j++) y[i][j] = bf2f(f2bf(y[i][j] * inv * nw[j]));
+                    for (int q = 0; q < 4; q++) { /* rounded to bf16 in pairs */
+                        const uint32_t w = pack_bf(y[i][2 * q] * inv * nw[2 * q],
+                                                   y[i][2 * q + 1] * inv * nw[2 * q + 1]);
+                        y[i][2 * q] = lo_bf(w);
+                        y[i][2 * q + 1] = hi_bf(w);
+                    }
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
                         const float y0 = y[i][2 * q] * rc[i][q] - y[i][2 * q + 1] * rs[i][q];

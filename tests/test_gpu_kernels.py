@@ -368,6 +368,9 @@ def test_linear_tile_walk(gpu, qd, oracle, epi):
 
 @pytest.mark.parametrize("rows,int8,rope_rows", [(300, False, 300), (300, True, 150),
                                                  (1000, True, 500), (4357, False, 4357),
+                                                 # tables under 128 rows: the plain
+                                                 # linear, then the standalone kernel
+                                                 (300, False, 100), (300, True, 64),
                                                  # 270 tiles: a tile walk whose last 14
                                                  # tiles run as half tiles
                                                  (11400, False, 11400)])
@@ -376,7 +379,7 @@ def test_linear_qknorm_epilogue_bit_identical(gpu, qd, oracle, rows, int8, rope_
     in its epilogue equals the linear followed by qw_gpu_qk_norm_rope_bf16,
     bit for bit (same sums, same reduction order, same roundings): fused
     int8 kernel, widen route, ragged rows, a RoPE table shorter than the
-    rows (batched sequences)."""
+    rows (batched sequences), tables shorter than a wave's 128 rows."""
     heads, k = 4, 512
     n = 3 * heads * 128
     x = synth(oracle, rows * k, 31)
