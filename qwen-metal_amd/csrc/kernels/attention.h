@@ -328,11 +328,12 @@ QW_KERNEL void __launch_bounds__(64 * ANW, 8 / ANW) qw_attention_bf16(qw_attn_ar
         /* The running max moves when the tile max exceeds it by more than 8
          * (log2 units), i.e. when some p would exceed 2^8; every p is at most
          * this half's sum of the rounded p, so a half whose sum stays below
-         * 256 needs no move. Only otherwise (and while the max is still
-         * -inf) is the tile max computed and the rule applied, with P
-         * recomputed after a move: the same P, l and O as applying the rule
-         * on every tile. */
-        if (__builtin_amdgcn_ballot_w64(rs >= 256.0f || m_run == -INFINITY)) {
+         * 256 needs no move. Only otherwise (and while the max of a row
+         * that sees any key is still -inf) is the tile max computed and the
+         * rule applied, with P recomputed after a move: the same P, l and O
+         * as applying the rule on every tile. A row that sees no key (past
+         * q_rows) keeps m = -inf, P = 0 and l = 0 either way. */
+        if (__builtin_amdgcn_ballot_w64(rs >= 256.0f || (m_run == -INFINITY && L != 0))) {
             float mt = -INFINITY;
 #pragma unroll
             for (int kbk = 0; kbk < AKB; kbk++)
