@@ -887,7 +887,7 @@ static int widen_launch(h3_gpu *g, uint16_t *out, const int8_t *in, size_t n) {
     wa.out = out;
     wa.in = in;
     wa.count = n;
-    unsigned blocks = (unsigned)std::min<size_t>((n / 16 + 255) / 256, 8192);
+    unsigned blocks = (unsigned)std::min<size_t>((n / 8 + 255) / 256, 65536);
     return launch(g, K_WIDEN, dim3(blocks ? blocks : 1), dim3(256), wa);
 }
 
