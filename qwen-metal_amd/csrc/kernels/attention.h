@@ -11,7 +11,8 @@
  * (column lane % 32) and 16 keys per 32-key block, so the row max / row sum
  * of the online softmax need at most one cross-half exchange (lane ^ 32)
  * instead of a 32-lane reduction (the max only when it moves, the sum once
- * at the end), and the per-query rescale of the output is a lane scalar. The output is accumulated transposed too, O^T = V^T P^T: the
+ * at the end), and the per-query rescale of the output is a lane scalar.
+ * The output is accumulated transposed too, O^T = V^T P^T: the
  * probabilities stay in registers and feed the MFMA B operand directly.
  * Within each 16-key K-step the keys are permuted identically in the V^T
  * (A) and P^T (B) operands, which leaves the contraction unchanged.

@@ -58,9 +58,9 @@ __device__ __forceinline__ bf16x8 i8x8_to_bf16(u32x2 q) {
 
 /* out[i] = bf16(q[i]) for count int8 weights (count % 16 == 0): the
  * unscaled widening that lets int8 linears run on the bf16 GEMM, whose
- * epilogue then applies the per-row scale to the fp32 sums. */
-/* 8 weights per thread and step (an 8-byte load, a 16-byte store):
- * measured 17-19% faster than 16 per step on the step's three weights */
+ * epilogue then applies the per-row scale to the fp32 sums. 8 weights per
+ * thread and step (an 8-byte load, a 16-byte store): measured 17-19%
+ * faster than 16 per step on the step's three weights. */
 QW_KERNEL void __launch_bounds__(256) qw_widen_i8_bf16(qw_widen_args a) {
     const uint64_t n8 = a.count / 8;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n8;
