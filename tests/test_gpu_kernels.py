@@ -119,9 +119,12 @@ def test_linear_store(gpu, qd, oracle, rows, k, n, bias, int8):
     assert_linear_close(oracle, got, ref.ravel(), mag)
 
 
-@pytest.mark.parametrize("int8,rows", [(False, 300), (True, 300), (True, 600), (False, 4),
-                                       (True, 7)])
-def test_linear_gelu_and_gate_epilogues(gpu, qd, oracle, int8, rows):
+@pytest.mark.parametrize("int8,rows,rm_blocks", [(False, 300, 0), (True, 300, 0), (True, 600, 0),
+                                                 (False, 4, 0), (True, 7, 0), (False, 300, 1),
+                                                 (True, 600, 1)])
+def test_linear_gelu_and_gate_epilogues(gpu, qd, oracle, int8, rows, rm_blocks):
+    """rm_blocks: gate rows constant over whole 128-row blocks but one (the
+    text/image boundary at row 200), as in the DiT's row map."""
     k, n = 512, 768
     x = synth(oracle, rows * k, 4)
     w = synth(oracle, n * k, 5, 0.02)
@@ -142,7 +145,7 @@ def test_linear_gelu_and_gate_epilogues(gpu, qd, oracle, int8, rows):
     # GATE: h = bf16(h + bf16(y) * gate[row_map[r], slot 2])
     slots = 6
     mod = synth(oracle, 2 * slots * n, 7, 0.5)
-    rm = (np.arange(rows) % 3 == 0).astype(np.uint32)
+    rm = ((np.arange(rows) >= 200) if rm_blocks else (np.arange(rows) % 3 == 0)).astype(np.uint32)
     h0 = synth(oracle, rows * n, 8)
     ht, mt, rmt = gpu.put(h0), gpu.put(mod), gpu.put(rm)
     gpu.linear(ht, xt, wt, rows, k, n, bias=bt, wscale=st, epilogue=qd.LINEAR_GATE,
@@ -181,6 +184,10 @@ SPLIT_CASES = [
     # 64 tiles, 4 pieces each: every CU runs one piece; ragged, int8 in LDS
     (2048, 8192, 2048, False, "gate"),
     (2000, 8192, 2000, True, "gelu"),
+    # gate rows constant over whole 128-row blocks but one (the text/image
+    # boundary at row 200), as in the DiT's row map
+    (512, 8192, 2048, True, "gate_blocks"),
+    (300, 4096, 1024, False, "gate_blocks"),
 ]
 
 
@@ -201,10 +208,11 @@ def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
     mag = oracle.bf16_to_f32(oracle.linear(absx, absw, None, rows, k, n)).ravel()
     outs = []
     for rep in range(2):  # piece counters must be back at 0 for the second call
-        if epi == "gate":
+        if epi in ("gate", "gate_blocks"):
             slots = 6
             mod = synth(oracle, 2 * slots * n, 14, 0.5)
-            rm = (np.arange(rows) % 3 == 1).astype(np.uint32)
+            rm = ((np.arange(rows) % 3 == 1) if epi == "gate" else
+                  (np.arange(rows) >= 200)).astype(np.uint32)
             h0 = synth(oracle, rows * n, 15)
             out = gpu.put(h0)
             gpu.linear(out, xt, wt, rows, k, n, bias=bt, wscale=st, epilogue=qd.LINEAR_GATE,
@@ -220,7 +228,7 @@ def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
     if epi == "store":
         assert_linear_close(oracle, got, lin.ravel(), mag)
         return
-    if epi == "gate":
+    if epi in ("gate", "gate_blocks"):
         # out = bf16(h + bf16(y) g): where h and y g nearly cancel, the one
         # flip of bf16(y) that a different summation order may cause moves
         # the output by many of its ulps, so accept the gate of y or of
