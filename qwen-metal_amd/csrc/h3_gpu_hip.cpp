@@ -29,7 +29,9 @@ enum {
     K_GEMM_BF16_STORE_Q, K_GEMM_BF16_GELU_Q, K_GEMM_BF16_GATE_Q, K_GEMM_BF16_QKN_Q,
     K_WIDEN, K_LN_MOD_WIDE, K_EULER, K_LORA,
     K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_ZERO,
-    K_GEMM_W8_STORE_Q, K_GEMM_W8_GELU_Q, K_GEMM_W8_GATE_Q, K_GEMM_W8_QKN_Q, K_COUNT
+    K_GEMM_W8_STORE_Q, K_GEMM_W8_GELU_Q, K_GEMM_W8_GATE_Q, K_GEMM_W8_QKN_Q,
+    K_GEMM_BF16_STORE_T224, K_GEMM_BF16_GELU_T224, K_GEMM_BF16_GATE_T224, K_GEMM_BF16_QKN_T224,
+    K_COUNT
 };
 static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_bf16", "qw_rms_norm_one_bf16", "qw_qk_norm_rope_bf16",
@@ -41,7 +43,9 @@ static const char *k_names[K_COUNT] = {
     "qw_layer_norm_mod_wide_bf16", "qw_cfg_euler_f32", "qw_lora_fuse_bf16",
     "qw_gemv_bf16_store", "qw_gemv_bf16_gelu", "qw_gemv_i8_store", "qw_gemv_i8_gelu",
     "qw_zero_u32",
-    "qw_gemm_w8_store_q", "qw_gemm_w8_gelu_q", "qw_gemm_w8_gate_q", "qw_gemm_w8_qkn_q"};
+    "qw_gemm_w8_store_q", "qw_gemm_w8_gelu_q", "qw_gemm_w8_gate_q", "qw_gemm_w8_qkn_q",
+    "qw_gemm_bf16_store_t224", "qw_gemm_bf16_gelu_t224", "qw_gemm_bf16_gate_t224",
+    "qw_gemm_bf16_qkn_t224"};
 
 /* How int8 linears run (QW_INT8_ROUTE, a measurement switch): AUTO (the
  * default) widens the weight to a bf16 copy and runs the bf16 kernels when
@@ -67,6 +71,7 @@ struct h3_gpu {
     size_t scratch_bytes;
     uint32_t attn_threads; /* attention workgroup size, 64 per 32-query wave */
     int int8_route; /* QW_INT8_* : how int8 linears of many rows run */
+    int t224;       /* 224-row tiles allowed (QW_GEMM_T224=0 turns them off, for measurement) */
     /* qw_gpu_span_*: event pairs recorded on the stream, read after a sync */
     hipEvent_t *span_ev;
     int *span_tag;
@@ -179,6 +184,8 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
         if (!strcmp(r, "w8")) g->int8_route = QW_INT8_W8;
         else if (!strcmp(r, "widen")) g->int8_route = QW_INT8_WIDEN;
     }
+    g->t224 = 1;
+    if (const char *r = getenv("QW_GEMM_T224")) g->t224 = atoi(r) != 0;
     g->cus = 0;
     g->sk_part = NULL;
     g->sk_flag = NULL;
@@ -1174,6 +1181,21 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * tile) */
     a.half_from = 0;
     a.half_count = 0;
+    if (a.split == 1 && !(int8 && !widen) && g->t224 && g->cus % 8 == 0) {
+        /* 224-row tiles where they leave fewer (work-weighted) waves than
+         * 256-row tiles with their half-tile tail: a wave of 224-row tiles
+         * is 0.875 of one of 256-row tiles. Out projection, M = 8704: 2
+         * waves of 0.875 (468 tiles) against 2 waves (408 tiles). */
+        const uint32_t C = g->cus, R = tiles % C;
+        const uint32_t t224 = ((d->rows + 223) / 224) * a.tiles_n;
+        const double w256 = (double)(tiles / C) + (R ? (2 * R <= C ? 0.5 : 1.0) : 0.0);
+        const double w224 = 0.875 * (double)((t224 + C - 1) / C);
+        if (w224 < 0.97 * w256) {
+            a.tiles_m = (d->rows + 223) / 224;
+            return launch(g, K_GEMM_BF16_STORE_T224 + d->epilogue, dim3(t224 < C ? t224 : C),
+                          dim3(threads), a);
+        }
+    }
     if (a.split == 1 && grid > g->cus && g->cus % 8 == 0) {
         grid = g->cus;
         /* a last wave of at most half the CUs' tiles runs as twice as many

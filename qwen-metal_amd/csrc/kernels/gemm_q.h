@@ -62,21 +62,28 @@ struct QgCtx {
  * reads it, and the compiler does not see the asm MFMAs to insert them. This
  * fence takes the fragments as inputs, so whatever writes them (int8
  * widening, register copies) is placed before it, and supplies the 2. */
+template <int N = 8>
 __device__ __forceinline__ void qg_ready(const bf16x8 (&f)[8]) {
-    asm volatile("s_nop 1" ::"v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "v"(f[4]), "v"(f[5]),
-                 "v"(f[6]), "v"(f[7]));
+    static_assert(N == 7 || N == 8, "fragment count");
+    if constexpr (N == 8)
+        asm volatile("s_nop 1" ::"v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "v"(f[4]), "v"(f[5]),
+                     "v"(f[6]), "v"(f[7]));
+    else
+        asm volatile("s_nop 1" ::"v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "v"(f[4]), "v"(f[5]),
+                     "v"(f[6]));
 }
 
 /* fragment j of a sub-step, in the order its MFMAs consume them (W block 0,
- * A blocks 0-7, W blocks 1-7) */
+ * A blocks 0..MB-1, W blocks 1-7) */
+template <int MB = 8>
 __device__ __forceinline__ void qg_read(const QgCtx &c, const unsigned char *cur, uint32_t ch,
                                         bf16x8 (&af)[8], bf16x8 (&bw)[8], int j) {
     if (j == 0)
         bw[0] = *(const bf16x8 *)(cur + QG_A_BYTES + c.w_frag + ch);
-    else if (j <= 8)
+    else if (j <= MB)
         af[j - 1] = *(const bf16x8 *)(cur + c.a_frag + (j - 1) * 2048 + ch);
     else
-        bw[j - 8] = *(const bf16x8 *)(cur + QG_A_BYTES + c.w_frag + (j - 8) * 2048 + ch);
+        bw[j - MB] = *(const bf16x8 *)(cur + QG_A_BYTES + c.w_frag + (j - MB) * 2048 + ch);
 }
 
 /* One 64-k slice: the stage `cur` is multiplied while slice k_next streams
@@ -87,70 +94,86 @@ __device__ __forceinline__ void qg_read(const QgCtx &c, const unsigned char *cur
  * direct loads issued back to back, than the loads spread over both
  * sub-steps, and than the read placed before the load); under the 64 MFMAs
  * of sub-step 0 the 16 fragments of sub-step 1 are read, one every 4 MFMAs. */
-template <bool PREV>
+template <bool PREV, int MB = 8>
 __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], bf16x8 (&pa)[8],
                                          bf16x8 (&pw)[8], const unsigned char *__restrict__ cur,
                                          unsigned char *__restrict__ nxt, uint32_t k_next) {
+    /* MB A blocks of 16 rows per wave (8: 256-row tiles, 7: 224-row
+     * tiles): 8 MB MFMAs per sub-step; MB + 8 direct loads (A, then W) and
+     * fragment reads, those past the one-per-4-MFMAs slots right after */
+    constexpr int NM = 8 * MB, NL = MB + 8;
     const uint32_t nl = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)nxt;
     auto dma = [&](int j) __attribute__((always_inline)) {
-        if (j < 8)
+        if (j < MB)
             gemm_dma16(c.a_rs4, nl + c.dst0 + j * 1024, c.a_dvoff[j], k_next * 2);
         else
-            gemm_dma16(c.w_rs4, nl + QG_A_BYTES + c.dst0 + (j - 8) * 1024, c.w_dvoff[j - 8],
-                       k_next * 2);
+            gemm_dma16(c.w_rs4, nl + QG_A_BYTES + (MB == 8 ? c.dst0 : c.wdst0) + (j - MB) * 1024,
+                       c.w_dvoff[j - MB], k_next * 2);
     };
     bf16x8 af[8], bw[8], af1[8], bw1[8];
     if (PREV) {
         qg_ready(pw);
-        qg_ready(pa);
+        qg_ready<MB>(pa);
 #pragma unroll
-        for (int i = 0; i < 64; i++) {
-            QG_MFMA(acc[i & 7][i >> 3], pw[i >> 3], pa[i & 7]);
+        for (int i = 0; i < NM; i++) {
+            QG_MFMA(acc[i % MB][i / MB], pw[i / MB], pa[i % MB]);
             if ((i & 3) == 1) dma(i >> 2);
-            if ((i & 3) == 3) qg_read(c, cur, c.ch[0], af, bw, i >> 2);
+            if ((i & 3) == 3) qg_read<MB>(c, cur, c.ch[0], af, bw, i >> 2);
+        }
+#pragma unroll
+        for (int j = NM / 4; j < NL; j++) {
+            dma(j);
+            qg_read<MB>(c, cur, c.ch[0], af, bw, j);
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < 16; j++) dma(j);
+        for (int j = 0; j < NL; j++) dma(j);
 #pragma unroll
-        for (int j = 0; j < 16; j++) qg_read(c, cur, c.ch[0], af, bw, j);
+        for (int j = 0; j < NL; j++) qg_read<MB>(c, cur, c.ch[0], af, bw, j);
     }
 #pragma unroll
-    for (int i = 0; i < 64; i++) {
+    for (int i = 0; i < NM; i++) {
         if (PREV)
-            QG_MFMA(acc[i & 7][i >> 3], bw[i >> 3], af[i & 7]);
+            QG_MFMA(acc[i % MB][i / MB], bw[i / MB], af[i % MB]);
         else
-            QG_MFMA0(acc[i & 7][i >> 3], bw[i >> 3], af[i & 7]);
-        if ((i & 3) == 3) qg_read(c, cur, c.ch[1], af1, bw1, i >> 2);
+            QG_MFMA0(acc[i % MB][i / MB], bw[i / MB], af[i % MB]);
+        if ((i & 3) == 3) qg_read<MB>(c, cur, c.ch[1], af1, bw1, i >> 2);
     }
 #pragma unroll
-    for (int i = 0; i < 8; i++) pa[i] = af1[i];
+    for (int j = NM / 4; j < NL; j++) qg_read<MB>(c, cur, c.ch[1], af1, bw1, j);
+#pragma unroll
+    for (int i = 0; i < MB; i++) pa[i] = af1[i];
 #pragma unroll
     for (int i = 0; i < 8; i++) pw[i] = bw1[i];
 }
 
 /* Sums of tile (tm, tn) over k-steps [kb, ke) into acc; ends with the LDS
- * stages free (after a barrier). */
+ * stages free (after a barrier). MB = 8: 256-row tiles; MB = 7: 224-row
+ * tiles (each wave's 112 rows; the A stage's last 32 rows unused). */
+template <int MB = 8>
 __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char *lds,
                                             unsigned char *lds_b, uint32_t tm, uint32_t tn,
                                             uint32_t kb, uint32_t ke, floatx4 (&acc)[8][8]) {
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave >> 1, wn = wave & 1;
-    const uint32_t m0 = tm * 256, n0 = tn * 256;
+    const uint32_t m0 = tm * (MB * 32), n0 = tn * 256;
     QgCtx c;
     const uint32_t lrow = lane >> 3, lp = lane & 7;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const uint32_t r = wave * 64 + j * 8 + lrow;
-        c.a_dvoff[j] = (min(m0 + r, a.m - 1) * a.lda + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+        const uint32_t ra = wave * (MB * 8) + j * 8 + lrow; /* A row: 8 MB rows per wave */
+        if (j < MB)
+            c.a_dvoff[j] = (min(m0 + ra, a.m - 1) * a.lda + (lp ^ ((ra >> 1) & 7u)) * 8) * 2;
         c.w_dvoff[j] = (min(n0 + r, a.n - 1) * a.k + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
     }
     c.a_rs4 = gemm_rs4(a.a, a.a_bytes);
     c.w_rs4 = gemm_rs4(a.w, a.w_bytes);
-    c.dst0 = wave * 64 * 128;
+    c.dst0 = wave * (MB * 8) * 128;
+    c.wdst0 = wave * 64 * 128;
     const uint32_t l16 = lane & 15, h = lane >> 4, swz = (l16 >> 1) & 7u;
-    c.a_frag = (wm * 128 + l16) * 128;
+    c.a_frag = (wm * (MB * 16) + l16) * 128;
     c.w_frag = (wn * 128 + l16) * 128;
     c.ch[0] = ((0 + h) ^ swz) << 4;
     c.ch[1] = ((4 + h) ^ swz) << 4;
@@ -159,31 +182,32 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
         const uint32_t nb =
             (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)lds;
 #pragma unroll
-        for (int j = 0; j < 8; j++)
+        for (int j = 0; j < MB; j++)
             gemm_dma16(c.a_rs4, nb + c.dst0 + j * 1024, c.a_dvoff[j], kb * GBK * 2);
 #pragma unroll
         for (int j = 0; j < 8; j++)
-            gemm_dma16(c.w_rs4, nb + QG_A_BYTES + c.dst0 + j * 1024, c.w_dvoff[j], kb * GBK * 2);
+            gemm_dma16(c.w_rs4, nb + QG_A_BYTES + (MB == 8 ? c.dst0 : c.wdst0) + j * 1024,
+                       c.w_dvoff[j], kb * GBK * 2);
     }
     QW_SLICE_END();
     bf16x8 pa[8], pw[8];
-    qg_slice<false>(c, acc, pa, pw, lds, lds_b, (kb + 1 < KT ? kb + 1 : kb) * GBK);
+    qg_slice<false, MB>(c, acc, pa, pw, lds, lds_b, (kb + 1 < KT ? kb + 1 : kb) * GBK);
     QW_SLICE_END();
     uint32_t kt = kb + 1;
     for (; kt + 1 < KT; kt += 2) {
-        qg_slice<true>(c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
+        qg_slice<true, MB>(c, acc, pa, pw, lds_b, lds, (kt + 1) * GBK);
         QW_SLICE_END();
-        qg_slice<true>(c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
+        qg_slice<true, MB>(c, acc, pa, pw, lds, lds_b, (kt + 2 < KT ? kt + 2 : kt + 1) * GBK);
         QW_SLICE_END();
     }
     if (kt < KT) {
-        qg_slice<true>(c, acc, pa, pw, lds_b, lds, kt * GBK);
+        qg_slice<true, MB>(c, acc, pa, pw, lds_b, lds, kt * GBK);
         QW_SLICE_END();
     }
     qg_ready(pw);
-    qg_ready(pa);
+    qg_ready<MB>(pa);
 #pragma unroll
-    for (int i = 0; i < 64; i++) QG_MFMA(acc[i & 7][i >> 3], pw[i >> 3], pa[i & 7]);
+    for (int i = 0; i < 8 * MB; i++) QG_MFMA(acc[i % MB][i / MB], pw[i / MB], pa[i % MB]);
     /* the epilogue reads the accumulators with ordinary instructions: let
      * the last MFMAs' results land first (the inline assembly hides them
      * from the compiler's hazard tracking) */
@@ -588,8 +612,9 @@ __device__ __forceinline__ void qg_mainloop_any(const qw_gemm_args &a, unsigned 
         qg_mainloop(a, lds, lds_b, tm, tn, kb, ke, acc);
 }
 
-/* The epilogue of the tile (MB = 8) or half tile (MB = 4) whose rows start
- * at m0 and columns at n0: each wave's MB x 8 accumulator blocks. */
+/* The epilogue of the tile (MB = 8), 224-row tile (MB = 7) or half tile
+ * (MB = 4) whose rows start at m0 and columns at n0: each wave's MB x 8
+ * accumulator blocks. */
 template <int EPI, int INT8, int MB>
 __device__ __forceinline__ void qg_finish_at(const qw_gemm_args &a, unsigned char *lds,
                                              unsigned char *lds_b, uint32_t m0, uint32_t n0,
@@ -605,10 +630,12 @@ __device__ __forceinline__ void qg_finish_at(const qw_gemm_args &a, unsigned cha
      * loop's last barrier), one 32-row slab (16.5 KB) at a time */
     float *region = (float *)((wave < 2 ? lds : lds_b) + (wave & 1) * REG);
     const uint32_t poff = wm * 128 * 256 + wn * 128;
-    /* slab mi: rows 32 mi + 16 q + lane % 16 (tile mb = 2 mi + q), columns
-     * 32 ni + 16 p + 4 (lane / 16) + 0..3 (tile nb = 2 ni + p). Columns
+    /* slab mi: rows SB 16 mi + 16 q + lane % 16 (tile mb = SB mi + q), columns
+     * 32 ni + 16 p + 4 (lane / 16) + 0..3 (tile nb = 2 ni + p); SB = 2 blocks
+     * of 16 rows per slab, 1 for an odd block count (224-row tiles). Columns
      * 64-127 are stored with the two 16-byte halves of each 32-byte group
      * exchanged (column c at c ^ 4). */
+    constexpr int SB = (MB & 1) ? 1 : 2;
     const uint32_t wc_lo = 4 * (lane >> 4), wc_hi = wc_lo ^ 4; /* column within 16, plain / exchanged */
     auto write_slab = [&](int mi) __attribute__((always_inline)) {
 #pragma unroll
@@ -616,9 +643,9 @@ __device__ __forceinline__ void qg_finish_at(const qw_gemm_args &a, unsigned cha
 #pragma unroll
             for (int p = 0; p < 2; p++)
 #pragma unroll
-                for (int q = 0; q < 2; q++)
+                for (int q = 0; q < SB; q++)
                     *(floatx4 *)(region + (16 * q + (lane & 15)) * LDF + ni * 32 + 16 * p +
-                                 (ni >= 2 ? wc_hi : wc_lo)) = acc[2 * mi + q][2 * ni + p];
+                                 (ni >= 2 ? wc_hi : wc_lo)) = acc[SB * mi + q][2 * ni + p];
     };
     /* the lane's 32 read-back bytes (columns 8 cc..8 cc + 7) as two
      * ds_read_b128: lanes 8-15 of a row (columns 64-127, stored exchanged)
@@ -634,7 +661,7 @@ __device__ __forceinline__ void qg_finish_at(const qw_gemm_args &a, unsigned cha
             v[4 + j] = v1[j];
         }
     };
-    gemm_epilogue_lds<EPI, INT8, MB / 2, 32, 8>(a, write_slab, read_row, row0, col0, lane,
+    gemm_epilogue_lds<EPI, INT8, MB / SB, 16 * SB, 4 * SB>(a, write_slab, read_row, row0, col0, lane,
                                             pst ? pst + poff : nullptr,
                                             pld ? pld + poff : nullptr, npart, own);
 }
@@ -715,6 +742,28 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
         __hip_atomic_store(a.sk_flag + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+/* 224-row tiles (bf16 W, no split tiles): one workgroup per CU walks the
+ * tiles, as the 256-row kernels do. Chosen where the tile count leaves a
+ * partly filled last wave that 224-row tiles avoid (the out projection at
+ * M = 8704: 468 tiles of 224 x 256 in 2 waves of 0.875 of a 256-row tile's
+ * work, against 408 tiles in 2 waves). */
+template <int EPI>
+__device__ __forceinline__ void qg_impl_t224(const qw_gemm_args &a, unsigned char *lds,
+                                             unsigned char *lds_b) {
+    const uint32_t KT = a.k / GBK;
+    const uint32_t nt = a.tiles_m * a.tiles_n;
+    floatx4 acc[8][8];
+    uint32_t tm, tn;
+    for (uint32_t id = blockIdx.x; id < nt; id += gridDim.x) {
+        uint32_t q = id;
+        if ((nt & 7u) == 0) q = (q & 7u) * (nt >> 3) + (q >> 3);
+        gemm_tile_at(a, q, tm, tn);
+        qg_mainloop<7>(a, lds, lds_b, tm, tn, 0, KT, acc);
+        qg_finish_at<EPI, 0, 7>(a, lds, lds_b, tm * 224, tn * 256, acc);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+}
+
 /* One LDS array fixes the layout: the first stage at offset 0, the second
  * at 64 KB, the split-tile counter after them. */
 #define QG_ENTRY(name, EPI, INT8)                                                              \
@@ -733,3 +782,13 @@ QG_ENTRY(qw_gemm_w8_store_q, QW_EPI_STORE, 1)
 QG_ENTRY(qw_gemm_w8_gelu_q, QW_EPI_GELU, 1)
 QG_ENTRY(qw_gemm_w8_gate_q, QW_EPI_GATE, 1)
 QG_ENTRY(qw_gemm_w8_qkn_q, QW_EPI_QKNORM, 1)
+/* bf16 W, 224-row tiles */
+#define QG_ENTRY_T224(name, EPI)                                                               \
+    QW_KERNEL void __launch_bounds__(256, 1) name(qw_gemm_args a) {                            \
+        __shared__ __attribute__((aligned(16))) unsigned char smem[2 * QG_STAGE + 16];          \
+        qg_impl_t224<EPI>(a, smem, smem + QG_STAGE);                                           \
+    }
+QG_ENTRY_T224(qw_gemm_bf16_store_t224, QW_EPI_STORE)
+QG_ENTRY_T224(qw_gemm_bf16_gelu_t224, QW_EPI_GELU)
+QG_ENTRY_T224(qw_gemm_bf16_gate_t224, QW_EPI_GATE)
+QG_ENTRY_T224(qw_gemm_bf16_qkn_t224, QW_EPI_QKNORM)

@@ -312,6 +312,81 @@ def test_linear_full_waves_never_split(qd, oracle):
     assert_linear_close(oracle, got[pick].ravel(), ref, mag)
 
 
+@pytest.mark.parametrize("rows,k,epi", [(4315, 512, "store"), (4315, 512, "gelu"),
+                                        (8604, 256, "gate"), (4315, 512, "qkn")])
+def test_linear_224_row_tiles(gpu, qd, oracle, rows, k, epi):
+    """Shapes whose 256 x 256 tiling leaves a partly filled last wave that
+    224 x 256 tiles avoid (on 256 CUs: 204 tiles of 256 rows, 1 wave, become
+    240 of 224 rows; 408 tiles, 2 waves, become 468 in 2 waves of 0.875 the
+    work): ragged rows through all four epilogues, against the oracle, and
+    the fused q/k norm + RoPE bit for bit against the plain linear followed
+    by the standalone kernel."""
+    n = 3072
+    x = synth(oracle, rows * k, 71)
+    w = synth(oracle, n * k, 72, 0.02)
+    b = synth(oracle, n, 73, 0.02)
+    xt, wt, bt = gpu.put(x), gpu.put(w), gpu.put(b)
+    lin = oracle.linear(x, w, b, rows, k, n)
+    absx, absw = x & np.uint16(0x7FFF), w & np.uint16(0x7FFF)
+    mag = oracle.bf16_to_f32(oracle.linear(absx, absw, None, rows, k, n)).ravel()
+    if epi == "qkn":
+        heads = n // 384
+        nq, nk = synth(oracle, 128, 74, 0.1), synth(oracle, 128, 75, 0.1)
+        ang = np.random.default_rng(76).uniform(-3, 3, (rows, 64)).astype(np.float32)
+        cos, sin = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+        nqt, nkt, ct, st_ = (gpu.put(v) for v in (nq, nk, cos, sin))
+        fused, ref = gpu.new(rows * n, qd.BF16), gpu.new(rows * n, qd.BF16)
+        gpu.linear(fused, xt, wt, rows, k, n, bias=bt, epilogue=qd.LINEAR_QKNORM,
+                   qknorm=(nqt, nkt, ct, st_, rows, 1e-6))
+        gpu.linear(ref, xt, wt, rows, k, n, bias=bt)
+        gpu.check(qd.lib().qw_gpu_qk_norm_rope_bf16(gpu.h, ref.h, rows, heads, n, n // 3, nqt.h,
+                                                     nkt.h, ct.h, st_.h, rows, 1e-6), "qk")
+        gpu.submit()
+        plain = gpu.new(rows * n, qd.BF16)
+        gpu.linear(plain, xt, wt, rows, k, n, bias=bt)
+        gpu.submit()
+        assert_linear_close(oracle, plain.read(), lin.ravel(), mag)
+        assert np.array_equal(fused.read(), ref.read())
+        return
+    if epi == "gate":
+        slots = 6
+        mod = synth(oracle, 2 * slots * n, 77, 0.5)
+        rm = (np.arange(rows) >= 200).astype(np.uint32)
+        h0 = synth(oracle, rows * n, 78)
+        out = gpu.put(h0)
+        gpu.linear(out, xt, wt, rows, k, n, bias=bt, epilogue=qd.LINEAR_GATE,
+                   modulation=gpu.put(mod), row_map=gpu.put(rm), slots=slots, gate_slot=2)
+    else:
+        out = gpu.new(rows * n, qd.BF16)
+        gpu.linear(out, xt, wt, rows, k, n, bias=bt,
+                   epilogue=qd.LINEAR_GELU if epi == "gelu" else qd.LINEAR_STORE)
+        if epi == "gelu":
+            want = np.empty_like(lin)
+            oracle.lib().qo_gelu_tanh(want.ravel(), lin.ravel(), lin.size)
+            want = want.ravel()
+    gpu.submit()
+    got = out.read()
+    if epi == "store":
+        assert_linear_close(oracle, got, lin.ravel(), mag)
+        return
+    if epi == "gate":
+        # where h and y g nearly cancel, one flip of bf16(y) moves the output
+        # by many of its ulps: accept the gate of y or of either bf16
+        # neighbour of y, each within one output ulp (as the split tiles)
+        best = None
+        for yv in (lin.ravel(),) + bf16_neighbours(lin.ravel()):
+            want = np.empty(rows * n, np.uint16)
+            oracle.lib().qo_gate(want, h0, np.ascontiguousarray(yv), mod, rm, rows, n, slots, 2)
+            d = ulp_diff(got, want)
+            best = d if best is None else np.minimum(best, d)
+        assert best.max() <= 1, best.max()
+        return
+    d = ulp_diff(got, want)
+    diff = np.abs(oracle.bf16_to_f32(got).astype(np.float64) - oracle.bf16_to_f32(want))
+    ok = (d <= 2) | (diff <= 2.0 ** -13 * mag)
+    assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
+
+
 @pytest.mark.parametrize("epi", ["store", "gelu", "gate"])
 def test_linear_tile_walk(gpu, qd, oracle, epi):
     """More tiles than compute units: the 16x16x32 GEMM launches one
