@@ -93,7 +93,9 @@ __device__ __forceinline__ void qg_read(const QgCtx &c, const unsigned char *cur
  * and one fragment read every 4 MFMAs (measured 7-10% faster than the 16
  * direct loads issued back to back, than the loads spread over both
  * sub-steps, and than the read placed before the load); under the 64 MFMAs
- * of sub-step 0 the 16 fragments of sub-step 1 are read, one every 4 MFMAs. */
+ * of sub-step 0 the 16 fragments of sub-step 1 are read, one every 4 MFMAs
+ * (256-row tiles; 224-row tiles: 56 MFMAs, 15 loads and reads, the last
+ * ones right after their MFMAs). */
 template <bool PREV, int MB = 8>
 __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], bf16x8 (&pa)[8],
                                          bf16x8 (&pw)[8], const unsigned char *__restrict__ cur,
