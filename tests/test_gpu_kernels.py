@@ -387,6 +387,31 @@ def test_linear_224_row_tiles(gpu, qd, oracle, rows, k, epi):
     assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
+@pytest.mark.parametrize("n,int8", [(1800, False), (1784, True)])
+def test_linear_224_row_tiles_ragged_cols(gpu, qd, oracle, n, int8):
+    """224-row tiles with a partial last tile column (N not a multiple of
+    256): 17 x 8 = 136 tiles of 256 rows (one wave, more than half full)
+    become 20 x 8 = 160 of 224 rows; int8 weights take the widening pass
+    (K < 8192, 512+ rows) into the same kernel."""
+    rows, k = 4315, 512
+    x = synth(oracle, rows * k, 81)
+    w = synth(oracle, n * k, 82, 0.02)
+    b = synth(oracle, n, 83, 0.02)
+    xt, bt = gpu.put(x), gpu.put(b)
+    out = gpu.new(rows * n, qd.BF16)
+    if int8:
+        q, s = oracle.quantize_int8_rows(w, n, k)
+        gpu.linear(out, xt, gpu.put(q), rows, k, n, bias=bt, wscale=gpu.put(s))
+        ref = oracle.linear_i8(x, q, s, b, rows, k, n)
+    else:
+        gpu.linear(out, xt, gpu.put(w), rows, k, n, bias=bt)
+        ref = oracle.linear(x, w, b, rows, k, n)
+    gpu.submit()
+    absx, absw = x & np.uint16(0x7FFF), w & np.uint16(0x7FFF)
+    mag = oracle.bf16_to_f32(oracle.linear(absx, absw, None, rows, k, n)).ravel()
+    assert_linear_close(oracle, out.read(), ref.ravel(), mag)
+
+
 @pytest.mark.parametrize("epi", ["store", "gelu", "gate"])
 def test_linear_tile_walk(gpu, qd, oracle, epi):
     """More tiles than compute units: the 16x16x32 GEMM launches one
