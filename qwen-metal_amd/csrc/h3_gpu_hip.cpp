@@ -72,6 +72,7 @@ struct h3_gpu {
     uint32_t attn_threads; /* attention workgroup size, 64 per 32-query wave */
     int int8_route; /* QW_INT8_* : how int8 linears of many rows run */
     int t224;       /* 224-row tiles allowed (QW_GEMM_T224=0 turns them off, for measurement) */
+    int half_small; /* launches of at most cus / 2 tiles as half tiles (QW_GEMM_HALF_SMALL=0: off) */
     /* qw_gpu_span_*: event pairs recorded on the stream, read after a sync */
     hipEvent_t *span_ev;
     int *span_tag;
@@ -186,6 +187,8 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     }
     g->t224 = 1;
     if (const char *r = getenv("QW_GEMM_T224")) g->t224 = atoi(r) != 0;
+    g->half_small = 1;
+    if (const char *r = getenv("QW_GEMM_HALF_SMALL")) g->half_small = atoi(r) != 0;
     g->cus = 0;
     g->sk_part = NULL;
     g->sk_flag = NULL;
@@ -1120,6 +1123,7 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     a.sk_part = NULL;
     a.sk_flag = NULL;
     uint32_t grid = tiles;
+    int small = 0;
     if (no_alloc) {
         const uint32_t s = split_choice(g, tiles, d->k / 64, QW_STATIC_PARTS);
         if (s > 1) {
@@ -1145,7 +1149,13 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
             grid = a.dp_tiles + R * s;
         }
     } else {
-        const uint32_t s = split_choice(g, tiles, d->k / 64);
+        /* a launch of at most half as many tiles as CUs (bf16-W kernels)
+         * runs as twice as many 128 x 256 half tiles, split in k-ranges
+         * where that pays (a half tile's split pieces also re-read half the
+         * partial bytes) */
+        small = !(int8 && !widen) && 2 * tiles <= g->cus && g->cus % 8 == 0 && g->half_small;
+        const uint32_t units = small ? 2 * tiles : tiles;
+        const uint32_t s = split_choice(g, units, d->k / 64);
         if (s > 1) {
             if (!g->sk_part) {
                 hipStreamSynchronize(g->stream);
@@ -1163,12 +1173,12 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
                     return fail(g, "linear: split-tile flag allocation failed");
                 }
             }
-            const uint32_t R = tiles % g->cus;
+            const uint32_t R = units % g->cus;
             /* the workspace holds QW_SPLIT_MAX_PIECES * cus partials and
              * cus counters; split_choice keeps within both */
             if ((uint64_t)R * s > (uint64_t)QW_SPLIT_MAX_PIECES * g->cus || R > g->cus)
                 return fail(g, "linear: %u x %u split pieces exceed the partial workspace", R, s);
-            a.dp_tiles = tiles - R;
+            a.dp_tiles = small ? 0 : tiles - R;
             a.split = s;
             a.sk_part = g->sk_part;
             a.sk_flag = g->sk_flag;
@@ -1181,6 +1191,15 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * tile) */
     a.half_from = 0;
     a.half_count = 0;
+    if (small) {
+        if (a.split > 1) {
+            a.half_count = 1; /* the split tiles run as half tiles */
+        } else {
+            a.half_count = 2 * tiles;
+            grid = 2 * tiles;
+        }
+        return launch(g, kid, dim3(grid), dim3(threads), a);
+    }
     if (a.split == 1 && !(int8 && !widen) && g->t224 && g->cus % 8 == 0) {
         /* 224-row tiles where they leave fewer (work-weighted) waves than
          * 256-row tiles with their half-tile tail: a wave of 224-row tiles

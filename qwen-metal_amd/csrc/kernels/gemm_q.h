@@ -64,10 +64,12 @@ struct QgCtx {
  * widening, register copies) is placed before it, and supplies the 2. */
 template <int N = 8>
 __device__ __forceinline__ void qg_ready(const bf16x8 (&f)[8]) {
-    static_assert(N == 7 || N == 8, "fragment count");
+    static_assert(N == 4 || N == 7 || N == 8, "fragment count");
     if constexpr (N == 8)
         asm volatile("s_nop 1" ::"v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "v"(f[4]), "v"(f[5]),
                      "v"(f[6]), "v"(f[7]));
+    else if constexpr (N == 4)
+        asm volatile("s_nop 1" ::"v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]));
     else
         asm volatile("s_nop 1" ::"v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "v"(f[4]), "v"(f[5]),
                      "v"(f[6]));
@@ -686,7 +688,10 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
     const uint32_t ndp = split ? a.dp_tiles : nt;
     floatx4 acc[8][8];
     uint32_t pid = blockIdx.x, tm, tn;
-    if (pid < ndp) {
+    /* no split tiles: the walk (its grid may exceed the tile count when the
+     * tiles run as half tiles); split: workgroups below ndp take a whole
+     * tile, the rest one piece */
+    if (!split || pid < ndp) {
         if (!split) {
             /* one workgroup per CU walks the tiles in strides of the grid;
              * id and id + grid sit on the same XCD (grid % 8 == 0). Tiles
@@ -719,17 +724,30 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
         qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc);
         return;
     }
-    /* piece of a split tile (k-range-major numbering, as gemm.h) */
+    /* piece of a split tile (k-range-major numbering, as gemm.h); with
+     * half_count set (bf16 W, a launch of at most half as many tiles as
+     * CUs) the split tiles run as half tiles, r = 2 tile + half */
     uint32_t &ticket = *(uint32_t *)(lds_b + QG_STAGE); /* reserved by QG_ENTRY */
-    const uint32_t R = nt - ndp, S = a.split, np = R * S;
+    const bool hs = !INT8 && a.half_count;
+    const uint32_t R = (nt - ndp) << (hs ? 1 : 0), S = a.split, np = R * S;
     uint32_t q = pid - ndp;
     if ((np & 7u) == 0) q = (q & 7u) * (np >> 3) + (q >> 3);
     const uint32_t piece = q / R, r = q % R;
     const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
-    gemm_tile_at(a, ndp + r, tm, tn);
-    qg_mainloop_any<INT8>(a, lds, lds_b, tm, tn, kb, ke, acc);
+    gemm_tile_at(a, ndp + (hs ? r >> 1 : r), tm, tn);
+    const uint32_t th = tm * 2 + (r & 1); /* half tile row (128 rows) */
     float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
-    qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc, slots + (size_t)piece * QW_SPLIT_PART);
+    if constexpr (!INT8) {
+        if (hs) {
+            qg_mainloop<4>(a, lds, lds_b, th, tn, kb, ke, acc);
+            qg_finish_at<EPI, INT8, 4>(a, lds, lds_b, th * 128, tn * 256, acc,
+                                       slots + (size_t)piece * QW_SPLIT_PART);
+        }
+    }
+    if (!hs) {
+        qg_mainloop_any<INT8>(a, lds, lds_b, tm, tn, kb, ke, acc);
+        qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc, slots + (size_t)piece * QW_SPLIT_PART);
+    }
     __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the partial's stores are done */
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
@@ -739,7 +757,12 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
     __syncthreads();
     if (ticket != S - 1) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S, piece);
+    if constexpr (!INT8) {
+        if (hs)
+            qg_finish_at<EPI, INT8, 4>(a, lds, lds_b, th * 128, tn * 256, acc, nullptr, slots, S,
+                                       piece);
+    }
+    if (!hs) qg_finish<EPI, INT8>(a, lds, lds_b, tm, tn, acc, nullptr, slots, S, piece);
     if (threadIdx.x == 0)
         __hip_atomic_store(a.sk_flag + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

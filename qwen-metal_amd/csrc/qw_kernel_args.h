@@ -48,7 +48,9 @@ typedef struct {
     uint32_t rope_rows, qk_cols;
     float eps;
     /* Tile walk (split <= 1, bf16 W): tiles [half_from, tiles) run as
-     * half_count = 2 (tiles - half_from) half tiles of 128 x 256; 0: none */
+     * half_count = 2 (tiles - half_from) half tiles of 128 x 256; 0: none.
+     * Split tiles (split > 1, bf16 W): half_count != 0 runs them as half
+     * tiles, each in `split` pieces. */
     uint32_t half_from, half_count;
 } qw_gemm_args;
 

@@ -251,13 +251,24 @@ def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
 
 @pytest.mark.parametrize("rows,k,n,epi", [(300, 3072, 1024, "gelu"), (1100, 12288, 768, "gate"),
                                           (2000, 8192, 2000, "store")])
-def test_int8_in_gemm_widening_bit_identical(gpu, qd, oracle, rows, k, n, epi):
+def test_int8_in_gemm_widening_bit_identical(qd, oracle, monkeypatch, rows, k, n, epi):
     """The int8 kernels that widen each W tile once per workgroup in LDS
     (taken below 512 rows and for K >= 8192) give the same bits as widening
     the weight to a bf16 copy (qw_gpu_widen_int8_bf16) and running the bf16
     kernel with the same row scales: the widening is exact and the scale
     multiplies the finished fp32 sums in both. Split tiles included
-    (K = 8192 and 12288)."""
+    (K = 8192 and 12288). Same k-ranges on both sides: the bf16 kernels'
+    half tiles for small launches (which may split K differently) are
+    turned off for this context."""
+    monkeypatch.setenv("QW_GEMM_HALF_SMALL", "0")
+    gpu = qd.Gpu()
+    try:
+        _widening_bit_identical(gpu, qd, oracle, rows, k, n, epi)
+    finally:
+        gpu.close()
+
+
+def _widening_bit_identical(gpu, qd, oracle, rows, k, n, epi):
     L = qd.lib()
     x = synth(oracle, rows * k, 61)
     w = synth(oracle, n * k, 62, 0.02)

@@ -88,7 +88,7 @@ def test_linear_static_two_contexts_in_flight(qd, oracle):
     still in flight, with no synchronisation between them. The per-device
     ordering makes the second call wait for the first, so both outputs equal
     those of the same calls run one at a time on the allocating entry
-    point, bit for bit (same split), and the workspace's counters are left
+    point (bit for bit where both split alike, else to the linear bar), and the workspace's counters are left
     at zero (a third call matches too)."""
     k, n, rows = 12288, 3072, 1152
     gpus = [qd.Gpu(), qd.Gpu()]
@@ -121,8 +121,10 @@ def test_linear_static_two_contexts_in_flight(qd, oracle):
     mag = None
     for i in range(2):
         if not np.array_equal(got[i], want[i]):
-            # the static form may split into fewer pieces than the allocating
-            # one (its workspace holds 128): then the linear bar applies
+            # the static form may split differently from the allocating one
+            # (its workspace holds 128 pieces; it runs whole tiles where the
+            # allocating one runs a small launch as half tiles): then the
+            # linear bar applies
             x = oracle.fill_normal_bf16(rows * k, SEED, 10 + i)
             w = oracle.fill_normal_bf16(n * k, SEED, 20 + i, 0.02)
             mag = oracle.bf16_to_f32(oracle.linear(x & np.uint16(0x7FFF), w & np.uint16(0x7FFF),
