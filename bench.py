@@ -290,6 +290,8 @@ def epilogue_operands(qd, gpu, M, R):
     weights with the joint RoPE tables."""
     H = CFG["hidden"]
     L = qd.lib()
+    if R != TEXT + GH * GW:  # the RoPE tables below are written for the module's geometry
+        raise ValueError(f"epilogue_operands: R = {R} is not {TEXT} + {GH} x {GW}")
     mod = gpu.new(2 * 6 * H, qd.BF16)
     gpu.check(L.qw_gpu_fill_normal_bf16(gpu.h, mod.h, 0, mod.n, 1, 5, 0.3, 0.0), "fill")
     rm = np.tile((np.arange(R) < TEXT).astype(np.uint32), M // R)

@@ -72,6 +72,7 @@ struct h3_gpu {
     uint32_t attn_threads; /* attention workgroup size, 64 per 32-query wave */
     int int8_route; /* QW_INT8_* : how int8 linears of many rows run */
     int t224;       /* 224-row tiles allowed (QW_GEMM_T224=0 turns them off, for measurement) */
+    uint32_t split_min_steps, split_force; /* measurement: QW_SPLIT_MIN_STEPS, QW_SPLIT_FORCE */
     int half_small; /* launches of at most cus / 2 tiles as half tiles (QW_GEMM_HALF_SMALL=0: off) */
     /* qw_gpu_span_*: event pairs recorded on the stream, read after a sync */
     hipEvent_t *span_ev;
@@ -187,6 +188,10 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     }
     g->t224 = 1;
     if (const char *r = getenv("QW_GEMM_T224")) g->t224 = atoi(r) != 0;
+    g->split_min_steps = 32;
+    if (const char *r = getenv("QW_SPLIT_MIN_STEPS")) g->split_min_steps = (uint32_t)atoi(r);
+    g->split_force = 0;
+    if (const char *r = getenv("QW_SPLIT_FORCE")) g->split_force = (uint32_t)atoi(r);
     g->half_small = 1;
     if (const char *r = getenv("QW_GEMM_HALF_SMALL")) g->half_small = atoi(r) != 0;
     g->cus = 0;
@@ -925,14 +930,20 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
  * 152 tail tiles in 3 pieces 557-588 us against 573-644 us for the
  * whole-tile walk, same boxes; 2, 4 or 5 pieces 595-660 us). Pieces stay at least 32 k-steps (2048 k) long: shorter
  * pieces lost more to their partials than they gained (K = 3072 linears
- * measured slower when split, K = 12288 ones faster), and
+ * measured slower when split, K = 12288 ones faster); the half tiles of a
+ * launch of at most cus / 2 tiles, whose pieces all run in one wave, go
+ * down to 16. And
  * R s <= QW_SPLIT_MAX_PIECES * cus bounds the partial workspace. */
 #define QW_SPLIT_MAX_PIECES 2
 static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps,
-                             uint64_t max_pieces = (uint64_t)QW_SPLIT_MAX_PIECES * 1024u) {
-    const uint32_t min_steps = 32;
+                             uint64_t max_pieces = (uint64_t)QW_SPLIT_MAX_PIECES * 1024u,
+                             uint32_t min_steps = 0) {
+    if (!min_steps) min_steps = g->split_min_steps;
     const uint32_t G = g->cus, R = tiles % G;
     if (R == 0) return 1; /* every wave is full: nothing to split */
+    if (g->split_force > 1 && (uint64_t)R * g->split_force <= (uint64_t)QW_SPLIT_MAX_PIECES * G &&
+        (uint64_t)R * g->split_force <= max_pieces && ksteps >= g->split_force)
+        return g->split_force;
     uint32_t best = 1;
     double best_t = 0.9;
     for (uint32_t s = 2; s <= 8; s++) {
@@ -1155,7 +1166,11 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
          * partial bytes) */
         small = !(int8 && !widen) && 2 * tiles <= g->cus && g->cus % 8 == 0 && g->half_small;
         const uint32_t units = small ? 2 * tiles : tiles;
-        const uint32_t s = split_choice(g, units, d->k / 64);
+        /* half tiles of a small launch: pieces down to 16 k-steps (M = 320,
+         * K = N = 3072: 24 half tiles in 3 pieces 33.4 us, unsplit 45.1;
+         * M = 1152: 60 in 2 pieces 45.3 against 48.1) */
+        const uint32_t s = split_choice(g, units, d->k / 64, (uint64_t)QW_SPLIT_MAX_PIECES * 1024u,
+                                        small ? 16u : 0u);
         if (s > 1) {
             if (!g->sk_part) {
                 hipStreamSynchronize(g->stream);

@@ -76,3 +76,15 @@ def ulp_diff(a, b):
         x = np.asarray(x, np.int32)
         return np.where(x & 0x8000, 0x8000 - (x & 0x7FFF), 0x8000 + (x & 0x7FFF))
     return np.abs(key(a) - key(b))
+
+
+def bf16_neighbours(v):
+    """The two bf16 values next to each element of v (bit patterns), by
+    magnitude one step down and one step up; around zero, +-the smallest
+    subnormal."""
+    v = v.astype(np.uint16)
+    mag = v & np.uint16(0x7FFF)
+    zero = mag == 0
+    down = np.where(zero, np.uint16(0x0001), v - np.uint16(1)).astype(np.uint16)
+    up = np.where(zero, np.uint16(0x8001), v + np.uint16(1)).astype(np.uint16)
+    return down, up

@@ -7,7 +7,7 @@ import math
 import numpy as np
 import pytest
 
-from conftest import cosine, read_bf16, rel_l2, ulp_diff
+from conftest import bf16_neighbours, cosine, read_bf16, rel_l2, ulp_diff
 
 pytestmark = pytest.mark.gpu
 SEED = 1234
@@ -50,18 +50,6 @@ def test_quantize_and_dequant_bit_exact(gpu, qd, oracle, rows, cols):
     assert np.array_equal(dq.read(), deq_ref)
 
 
-def bf16_neighbours(v):
-    """The two bf16 values next to each element of v (bit patterns), by
-    magnitude one step down and one step up; around zero, +-the smallest
-    subnormal."""
-    v = v.astype(np.uint16)
-    mag = v & np.uint16(0x7FFF)
-    zero = mag == 0
-    down = np.where(zero, np.uint16(0x0001), v - np.uint16(1)).astype(np.uint16)
-    up = np.where(zero, np.uint16(0x8001), v + np.uint16(1)).astype(np.uint16)
-    return down, up
-
-
 def assert_linear_close(oracle, got, ref, mag):
     """Two fp32 sums of the same bf16 products in different orders round
     to bf16 at most one ulp apart, except where cancellation leaves a
@@ -74,6 +62,27 @@ def assert_linear_close(oracle, got, ref, mag):
     ok = (d <= 1) | (diff <= 2.0 ** -14 * mag)
     assert ok.all(), (d.max(), np.flatnonzero(~ok)[:5])
     assert np.mean(d == 0) > 0.98
+
+
+def assert_gelu_close(oracle, got, lin, mag):
+    """bf16(gelu(y)), y = bf16(sum): where the sum sits at a rounding
+    boundary of y, another summation order rounds y the other way (one bf16
+    ulp of y), and gelu moves by up to 1.13 ulp(y) -- 3 output ulps where
+    gelu(y) falls into the binade below y (y = 2.016 / 2.031 -> 1.969 /
+    1.992). Accept gelu of y or of either bf16 neighbour of y within 2
+    output ulps, or the accumulation bound."""
+    lin = np.ascontiguousarray(lin.ravel())
+    best, plain = None, None
+    for yv in (lin,) + bf16_neighbours(lin):
+        want = np.empty_like(lin)
+        oracle.lib().qo_gelu_tanh(want, np.ascontiguousarray(yv), lin.size)
+        d = ulp_diff(got, want)
+        if plain is None:
+            plain = want
+        best = d if best is None else np.minimum(best, d)
+    diff = np.abs(oracle.bf16_to_f32(got).astype(np.float64) - oracle.bf16_to_f32(plain))
+    ok = (best <= 2) | (diff <= 2.0 ** -13 * mag)
+    assert ok.all() and np.mean(ulp_diff(got, plain) == 0) > 0.97, (best.max(), np.flatnonzero(~ok)[:5])
 
 
 LINEAR_CASES = [
@@ -241,12 +250,7 @@ def test_linear_split_tiles(gpu, qd, oracle, rows, k, n, int8, epi):
             best = d if best is None else np.minimum(best, d)
         assert best.max() <= 1, best.max()
         return
-    want = np.empty_like(lin)
-    oracle.lib().qo_gelu_tanh(want.ravel(), lin.ravel(), lin.size)
-    d = ulp_diff(got, want.ravel())
-    diff = np.abs(oracle.bf16_to_f32(got).astype(np.float64) - oracle.bf16_to_f32(want.ravel()))
-    ok = (d <= 2) | (diff <= 2.0 ** -13 * mag)
-    assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
+    assert_gelu_close(oracle, got, lin, mag)
 
 
 @pytest.mark.parametrize("rows,k,n,epi", [(300, 3072, 1024, "gelu"), (1100, 12288, 768, "gate"),
@@ -371,14 +375,13 @@ def test_linear_224_row_tiles(gpu, qd, oracle, rows, k, epi):
         out = gpu.new(rows * n, qd.BF16)
         gpu.linear(out, xt, wt, rows, k, n, bias=bt,
                    epilogue=qd.LINEAR_GELU if epi == "gelu" else qd.LINEAR_STORE)
-        if epi == "gelu":
-            want = np.empty_like(lin)
-            oracle.lib().qo_gelu_tanh(want.ravel(), lin.ravel(), lin.size)
-            want = want.ravel()
     gpu.submit()
     got = out.read()
     if epi == "store":
         assert_linear_close(oracle, got, lin.ravel(), mag)
+        return
+    if epi == "gelu":
+        assert_gelu_close(oracle, got, lin, mag)
         return
     if epi == "gate":
         # where h and y g nearly cancel, one flip of bf16(y) moves the output
@@ -391,11 +394,6 @@ def test_linear_224_row_tiles(gpu, qd, oracle, rows, k, epi):
             d = ulp_diff(got, want)
             best = d if best is None else np.minimum(best, d)
         assert best.max() <= 1, best.max()
-        return
-    d = ulp_diff(got, want)
-    diff = np.abs(oracle.bf16_to_f32(got).astype(np.float64) - oracle.bf16_to_f32(want))
-    ok = (d <= 2) | (diff <= 2.0 ** -13 * mag)
-    assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
 @pytest.mark.parametrize("n,int8", [(1800, False), (1784, True)])

@@ -1,12 +1,14 @@
 """qw_gpu_linear_static (the entry point that allocates nothing) against
 qw_gpu_linear on the same inputs, through the C-ABI: two calls in a row,
 the second on a smaller input, each within one bf16 ulp of the allocating
-entry point (or within 2^-14 sum |x||w| where the sum cancels), and no
+entry point (or within 2^-14 sum |x||w| where the sum cancels; with the
+residual gate, both within one ulp of the oracle's gate of y or of a bf16
+neighbour of y), and no
 device allocation by the runtime across the static calls."""
 import numpy as np
 import pytest
 
-from conftest import ulp_diff
+from conftest import bf16_neighbours, ulp_diff
 
 pytestmark = pytest.mark.gpu
 SEED = 77
@@ -74,6 +76,27 @@ def test_linear_static_matches_linear(qd, oracle, k, n, int8, epi, m1, m2):
                     assert grew
                 outs[no_alloc].append(out.read())
         for i, rows in enumerate((m1, m2)):
+            if epi == "gate":
+                # the entry points may split K differently (the allocating
+                # one runs a small launch as half tiles in k-ranges), so
+                # bf16(y) can round the other way at a rounding boundary;
+                # where h + y g cancels, that moves the output by many of its
+                # ulps. Both hold the gate of the oracle's y or of either bf16
+                # neighbour of y within one output ulp.
+                xs = x[:rows * k].copy()
+                lin = (oracle.linear_i8(xs, q, s, b, rows, k, n) if int8 else
+                       oracle.linear(xs, w, b, rows, k, n)).ravel()
+                h0 = res[:rows * n].copy()
+                for got in (outs[True][i], outs[False][i]):
+                    best = None
+                    for yv in (lin,) + bf16_neighbours(lin):
+                        want = np.empty(rows * n, np.uint16)
+                        oracle.lib().qo_gate(want, h0, np.ascontiguousarray(yv), gmod,
+                                             np.ascontiguousarray(rm[:rows]), rows, n, 4, 2)
+                        d = ulp_diff(got, want)
+                        best = d if best is None else np.minimum(best, d)
+                    assert best.max() <= 1, best.max()
+                continue
             mag = oracle.bf16_to_f32(oracle.linear(absx[:rows * k].copy(), absw, None, rows, k,
                                                    n)).ravel()
             _close(oracle, outs[True][i], outs[False][i], mag, epi)
