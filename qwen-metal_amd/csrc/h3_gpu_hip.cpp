@@ -31,6 +31,7 @@ enum {
     K_GEMV_BF16_STORE, K_GEMV_BF16_GELU, K_GEMV_I8_STORE, K_GEMV_I8_GELU, K_ZERO,
     K_GEMM_W8_STORE_Q, K_GEMM_W8_GELU_Q, K_GEMM_W8_GATE_Q, K_GEMM_W8_QKN_Q,
     K_GEMM_BF16_STORE_T224, K_GEMM_BF16_GELU_T224, K_GEMM_BF16_GATE_T224, K_GEMM_BF16_QKN_T224,
+    K_GEMM_BF16_STORE_H3, K_GEMM_BF16_GELU_H3, K_GEMM_BF16_GATE_H3, K_GEMM_BF16_QKN_H3,
     K_COUNT
 };
 static const char *k_names[K_COUNT] = {
@@ -45,7 +46,9 @@ static const char *k_names[K_COUNT] = {
     "qw_zero_u32",
     "qw_gemm_w8_store_q", "qw_gemm_w8_gelu_q", "qw_gemm_w8_gate_q", "qw_gemm_w8_qkn_q",
     "qw_gemm_bf16_store_t224", "qw_gemm_bf16_gelu_t224", "qw_gemm_bf16_gate_t224",
-    "qw_gemm_bf16_qkn_t224"};
+    "qw_gemm_bf16_qkn_t224",
+    "qw_gemm_bf16_store_h3", "qw_gemm_bf16_gelu_h3", "qw_gemm_bf16_gate_h3",
+    "qw_gemm_bf16_qkn_h3"};
 
 /* How int8 linears run (QW_INT8_ROUTE, a measurement switch): AUTO (the
  * default) widens the weight to a bf16 copy and runs the bf16 kernels when
@@ -73,6 +76,7 @@ struct h3_gpu {
     int int8_route; /* QW_INT8_* : how int8 linears of many rows run */
     int t224;       /* 224-row tiles allowed (QW_GEMM_T224=0 turns them off, for measurement) */
     uint32_t split_min_steps, split_force; /* measurement: QW_SPLIT_MIN_STEPS, QW_SPLIT_FORCE */
+    int half3;      /* small launches' half tiles on the three-stage kernels (QW_GEMM_HALF3=0: two) */
     int half_small; /* launches of at most cus / 2 tiles as half tiles (QW_GEMM_HALF_SMALL=0: off) */
     /* qw_gpu_span_*: event pairs recorded on the stream, read after a sync */
     hipEvent_t *span_ev;
@@ -192,6 +196,8 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     if (const char *r = getenv("QW_SPLIT_MIN_STEPS")) g->split_min_steps = (uint32_t)atoi(r);
     g->split_force = 0;
     if (const char *r = getenv("QW_SPLIT_FORCE")) g->split_force = (uint32_t)atoi(r);
+    g->half3 = 1;
+    if (const char *r = getenv("QW_GEMM_HALF3")) g->half3 = atoi(r) != 0;
     g->half_small = 1;
     if (const char *r = getenv("QW_GEMM_HALF_SMALL")) g->half_small = atoi(r) != 0;
     g->cus = 0;
@@ -1207,6 +1213,9 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     a.half_from = 0;
     a.half_count = 0;
     if (small) {
+        if (g->half3) /* one half tile (or piece of one) per workgroup, three stages */
+            return launch(g, K_GEMM_BF16_STORE_H3 + d->epilogue,
+                          dim3(2 * tiles * (a.split > 1 ? a.split : 1)), dim3(threads), a);
         if (a.split > 1) {
             a.half_count = 1; /* the split tiles run as half tiles */
         } else {

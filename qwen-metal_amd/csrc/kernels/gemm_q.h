@@ -77,15 +77,15 @@ __device__ __forceinline__ void qg_ready(const bf16x8 (&f)[8]) {
 
 /* fragment j of a sub-step, in the order its MFMAs consume them (W block 0,
  * A blocks 0..MB-1, W blocks 1-7) */
-template <int MB = 8>
+template <int MB = 8, int AB = QG_A_BYTES>
 __device__ __forceinline__ void qg_read(const QgCtx &c, const unsigned char *cur, uint32_t ch,
                                         bf16x8 (&af)[8], bf16x8 (&bw)[8], int j) {
     if (j == 0)
-        bw[0] = *(const bf16x8 *)(cur + QG_A_BYTES + c.w_frag + ch);
+        bw[0] = *(const bf16x8 *)(cur + AB + c.w_frag + ch);
     else if (j <= MB)
         af[j - 1] = *(const bf16x8 *)(cur + c.a_frag + (j - 1) * 2048 + ch);
     else
-        bw[j - MB] = *(const bf16x8 *)(cur + QG_A_BYTES + c.w_frag + (j - MB) * 2048 + ch);
+        bw[j - MB] = *(const bf16x8 *)(cur + AB + c.w_frag + (j - MB) * 2048 + ch);
 }
 
 /* One 64-k slice: the stage `cur` is multiplied while slice k_next streams
@@ -98,7 +98,7 @@ __device__ __forceinline__ void qg_read(const QgCtx &c, const unsigned char *cur
  * of sub-step 0 the 16 fragments of sub-step 1 are read, one every 4 MFMAs
  * (256-row tiles; 224-row tiles: 56 MFMAs, 15 loads and reads, the last
  * ones right after their MFMAs). */
-template <bool PREV, int MB = 8>
+template <bool PREV, int MB = 8, int AB = QG_A_BYTES>
 __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], bf16x8 (&pa)[8],
                                          bf16x8 (&pw)[8], const unsigned char *__restrict__ cur,
                                          unsigned char *__restrict__ nxt, uint32_t k_next) {
@@ -111,7 +111,7 @@ __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
         if (j < MB)
             gemm_dma16(c.a_rs4, nl + c.dst0 + j * 1024, c.a_dvoff[j], k_next * 2);
         else
-            gemm_dma16(c.w_rs4, nl + QG_A_BYTES + (MB == 8 ? c.dst0 : c.wdst0) + (j - MB) * 1024,
+            gemm_dma16(c.w_rs4, nl + AB + (MB == 8 ? c.dst0 : c.wdst0) + (j - MB) * 1024,
                        c.w_dvoff[j - MB], k_next * 2);
     };
     bf16x8 af[8], bw[8], af1[8], bw1[8];
@@ -122,18 +122,18 @@ __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
         for (int i = 0; i < NM; i++) {
             QG_MFMA(acc[i % MB][i / MB], pw[i / MB], pa[i % MB]);
             if ((i & 3) == 1) dma(i >> 2);
-            if ((i & 3) == 3) qg_read<MB>(c, cur, c.ch[0], af, bw, i >> 2);
+            if ((i & 3) == 3) qg_read<MB, AB>(c, cur, c.ch[0], af, bw, i >> 2);
         }
 #pragma unroll
         for (int j = NM / 4; j < NL; j++) {
             dma(j);
-            qg_read<MB>(c, cur, c.ch[0], af, bw, j);
+            qg_read<MB, AB>(c, cur, c.ch[0], af, bw, j);
         }
     } else {
 #pragma unroll
         for (int j = 0; j < NL; j++) dma(j);
 #pragma unroll
-        for (int j = 0; j < NL; j++) qg_read<MB>(c, cur, c.ch[0], af, bw, j);
+        for (int j = 0; j < NL; j++) qg_read<MB, AB>(c, cur, c.ch[0], af, bw, j);
     }
 #pragma unroll
     for (int i = 0; i < NM; i++) {
@@ -141,10 +141,10 @@ __device__ __forceinline__ void qg_slice(const QgCtx &c, floatx4 (&acc)[8][8], b
             QG_MFMA(acc[i % MB][i / MB], bw[i / MB], af[i % MB]);
         else
             QG_MFMA0(acc[i % MB][i / MB], bw[i / MB], af[i % MB]);
-        if ((i & 3) == 3) qg_read<MB>(c, cur, c.ch[1], af1, bw1, i >> 2);
+        if ((i & 3) == 3) qg_read<MB, AB>(c, cur, c.ch[1], af1, bw1, i >> 2);
     }
 #pragma unroll
-    for (int j = NM / 4; j < NL; j++) qg_read<MB>(c, cur, c.ch[1], af1, bw1, j);
+    for (int j = NM / 4; j < NL; j++) qg_read<MB, AB>(c, cur, c.ch[1], af1, bw1, j);
 #pragma unroll
     for (int i = 0; i < MB; i++) pa[i] = af1[i];
 #pragma unroll
@@ -216,6 +216,89 @@ __device__ __forceinline__ void qg_mainloop(const qw_gemm_args &a, unsigned char
      * the last MFMAs' results land first (the inline assembly hides them
      * from the compiler's hazard tracking) */
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+}
+
+/* Half tiles (MB = 4) with three LDS stages of 48 KB (A 16 KB, then W
+ * 32 KB), loads two slices ahead: for launches of at most half as many
+ * tiles as CUs, whose slices are bound by the load latency rather than the
+ * MFMAs (one slice ahead, a 128 x 256 slice takes most of a 256 x 256
+ * slice's time). Slice j is computed from stage j % 3 while slice j + 2
+ * streams into stage (j + 2) % 3, the stage slice j - 1 was computed from;
+ * each slice ends waiting for all but the newest slice's loads. Slices past
+ * ke - 1 reload ke - 1 so that every slice issues the same loads. Ends
+ * with the LDS free (all loads landed, after a barrier). */
+#define QG3_AB (4 * 32 * 128)         /* A bytes per stage: 128 rows x 64 bf16 */
+#define QG3_STAGE (QG3_AB + 256 * 128) /* + W: 256 rows x 64 bf16 */
+#define QG3_WAIT_NEWEST() asm volatile("s_waitcnt vmcnt(12) lgkmcnt(0)\n\ts_barrier" ::: "memory")
+__device__ __forceinline__ void qg_mainloop3(const qw_gemm_args &a, unsigned char *lds,
+                                             uint32_t th, uint32_t tn, uint32_t kb, uint32_t ke,
+                                             floatx4 (&acc)[8][8]) {
+    constexpr int MB = 4, NL = MB + 8; /* 12 loads per slice and thread: QG3_WAIT_NEWEST */
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave >> 1, wn = wave & 1;
+    const uint32_t m0 = th * 128, n0 = tn * 256;
+    QgCtx c;
+    const uint32_t lrow = lane >> 3, lp = lane & 7;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const uint32_t r = wave * 64 + j * 8 + lrow;
+        const uint32_t ra = wave * (MB * 8) + j * 8 + lrow;
+        if (j < MB)
+            c.a_dvoff[j] = (min(m0 + ra, a.m - 1) * a.lda + (lp ^ ((ra >> 1) & 7u)) * 8) * 2;
+        c.w_dvoff[j] = (min(n0 + r, a.n - 1) * a.k + (lp ^ ((r >> 1) & 7u)) * 8) * 2;
+    }
+    c.a_rs4 = gemm_rs4(a.a, a.a_bytes);
+    c.w_rs4 = gemm_rs4(a.w, a.w_bytes);
+    c.dst0 = wave * (MB * 8) * 128;
+    c.wdst0 = wave * 64 * 128;
+    const uint32_t l16 = lane & 15, h = lane >> 4, swz = (l16 >> 1) & 7u;
+    c.a_frag = (wm * (MB * 16) + l16) * 128;
+    c.w_frag = (wn * 128 + l16) * 128;
+    c.ch[0] = ((0 + h) ^ swz) << 4;
+    c.ch[1] = ((4 + h) ^ swz) << 4;
+    unsigned char *s0 = lds, *s1 = lds + QG3_STAGE, *s2 = lds + 2 * QG3_STAGE;
+    const uint32_t last = ke - 1;
+    auto issue = [&](unsigned char *st, uint32_t k) __attribute__((always_inline)) {
+        const uint32_t nb =
+            (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char *)st;
+#pragma unroll
+        for (int j = 0; j < MB; j++)
+            gemm_dma16(c.a_rs4, nb + c.dst0 + j * 1024, c.a_dvoff[j], k * GBK * 2);
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            gemm_dma16(c.w_rs4, nb + QG3_AB + c.wdst0 + j * 1024, c.w_dvoff[j], k * GBK * 2);
+    };
+    issue(s0, kb);
+    issue(s1, min(kb + 1, last));
+    QG3_WAIT_NEWEST(); /* slice kb landed */
+    bf16x8 pa[8], pw[8];
+    qg_slice<false, MB, QG3_AB>(c, acc, pa, pw, s0, s2, min(kb + 2, last) * GBK);
+    QG3_WAIT_NEWEST(); /* slice kb + 1 landed */
+    uint32_t kt = kb + 1;
+    for (; kt + 2 < ke; kt += 3) {
+        qg_slice<true, MB, QG3_AB>(c, acc, pa, pw, s1, s0, min(kt + 2, last) * GBK);
+        QG3_WAIT_NEWEST();
+        qg_slice<true, MB, QG3_AB>(c, acc, pa, pw, s2, s1, min(kt + 3, last) * GBK);
+        QG3_WAIT_NEWEST();
+        qg_slice<true, MB, QG3_AB>(c, acc, pa, pw, s0, s2, min(kt + 4, last) * GBK);
+        QG3_WAIT_NEWEST();
+    }
+    /* the last 0-2 slices, in the rotation's order */
+    if (kt < ke) {
+        qg_slice<true, MB, QG3_AB>(c, acc, pa, pw, s1, s0, min(kt + 2, last) * GBK);
+        QG3_WAIT_NEWEST();
+    }
+    if (kt + 1 < ke) {
+        qg_slice<true, MB, QG3_AB>(c, acc, pa, pw, s2, s1, min(kt + 3, last) * GBK);
+        QG3_WAIT_NEWEST();
+    }
+    qg_ready(pw);
+    qg_ready<MB>(pa);
+#pragma unroll
+    for (int i = 0; i < 8 * MB; i++) QG_MFMA(acc[i % MB][i / MB], pw[i / MB], pa[i % MB]);
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    QW_SLICE_END(); /* the reloads past ke - 1 land before the epilogue uses the LDS */
 }
 
 /* int8 W widened once per workgroup (the "_w8" kernels): the bf16 kernel's
@@ -789,6 +872,48 @@ __device__ __forceinline__ void qg_impl_t224(const qw_gemm_args &a, unsigned cha
     }
 }
 
+/* Small launches (at most cus / 2 tiles, bf16 W) as half tiles on the
+ * three-stage loop, one half tile -- or one k-range piece of one, when
+ * a.split > 1 -- per workgroup: grid = 2 tiles x split. Pieces meet as in
+ * qg_impl (k-range-major numbering, the last one in adds them in piece
+ * order and runs the epilogue). */
+template <int EPI>
+__device__ __forceinline__ void qg_impl_h3(const qw_gemm_args &a, unsigned char *lds) {
+    const uint32_t KT = a.k / GBK;
+    const uint32_t R = 2 * a.tiles_m * a.tiles_n, S = a.split > 1 ? a.split : 1, np = R * S;
+    uint32_t q = blockIdx.x;
+    if (q >= np) return;
+    if ((np & 7u) == 0) q = (q & 7u) * (np >> 3) + (q >> 3);
+    const uint32_t piece = q / R, r = q % R;
+    const uint32_t kb = piece * KT / S, ke = (piece + 1) * KT / S;
+    uint32_t tm, tn;
+    gemm_tile_at(a, r >> 1, tm, tn);
+    const uint32_t th = tm * 2 + (r & 1);
+    floatx4 acc[8][8];
+    qg_mainloop3(a, lds, th, tn, kb, ke, acc);
+    unsigned char *lds_b = lds + QG_STAGE;
+    if (S == 1) {
+        qg_finish_at<EPI, 0, 4>(a, lds, lds_b, th * 128, tn * 256, acc);
+        return;
+    }
+    uint32_t &ticket = *(uint32_t *)(lds + 3 * QG3_STAGE); /* reserved by QG_ENTRY_H3 */
+    float *slots = a.sk_part + (size_t)r * S * QW_SPLIT_PART;
+    qg_finish_at<EPI, 0, 4>(a, lds, lds_b, th * 128, tn * 256, acc,
+                            slots + (size_t)piece * QW_SPLIT_PART);
+    __builtin_amdgcn_s_waitcnt(0x0F70); /* vmcnt(0): the partial's stores are done */
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        ticket = __hip_atomic_fetch_add(a.sk_flag + r, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (ticket != S - 1) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    qg_finish_at<EPI, 0, 4>(a, lds, lds_b, th * 128, tn * 256, acc, nullptr, slots, S, piece);
+    if (threadIdx.x == 0)
+        __hip_atomic_store(a.sk_flag + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 /* One LDS array fixes the layout: the first stage at offset 0, the second
  * at 64 KB, the split-tile counter after them. */
 #define QG_ENTRY(name, EPI, INT8)                                                              \
@@ -817,3 +942,13 @@ QG_ENTRY_T224(qw_gemm_bf16_store_t224, QW_EPI_STORE)
 QG_ENTRY_T224(qw_gemm_bf16_gelu_t224, QW_EPI_GELU)
 QG_ENTRY_T224(qw_gemm_bf16_gate_t224, QW_EPI_GATE)
 QG_ENTRY_T224(qw_gemm_bf16_qkn_t224, QW_EPI_QKNORM)
+/* bf16 W, small launches: half tiles on three stages */
+#define QG_ENTRY_H3(name, EPI)                                                                 \
+    QW_KERNEL void __launch_bounds__(256, 1) name(qw_gemm_args a) {                            \
+        __shared__ __attribute__((aligned(16))) unsigned char smem[3 * QG3_STAGE + 16];         \
+        qg_impl_h3<EPI>(a, smem);                                                              \
+    }
+QG_ENTRY_H3(qw_gemm_bf16_store_h3, QW_EPI_STORE)
+QG_ENTRY_H3(qw_gemm_bf16_gelu_h3, QW_EPI_GELU)
+QG_ENTRY_H3(qw_gemm_bf16_gate_h3, QW_EPI_GATE)
+QG_ENTRY_H3(qw_gemm_bf16_qkn_h3, QW_EPI_QKNORM)
