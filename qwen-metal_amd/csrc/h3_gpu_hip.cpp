@@ -1212,6 +1212,7 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * tile) */
     a.half_from = 0;
     a.half_count = 0;
+    a.half3 = g->half3;
     if (small) {
         if (g->half3) /* one half tile (or piece of one) per workgroup, three stages */
             return launch(g, K_GEMM_BF16_STORE_H3 + d->epilogue,

@@ -794,7 +794,10 @@ __device__ __forceinline__ void qg_impl(const qw_gemm_args &a, unsigned char *ld
                     if ((H & 15u) == 0) hq = (hq & 7u) * (H >> 3) + (hq >> 3);
                     gemm_tile_at(a, F + (hq >> 1), tm, tn);
                     const uint32_t m0 = tm * 256 + (hq & 1) * 128;
-                    qh_mainloop(a, lds, lds_b, m0, tn * 256, acc);
+                    if (a.half3)
+                        qg_mainloop3(a, lds, m0 / 128, tn, 0, KT, acc);
+                    else
+                        qh_mainloop(a, lds, lds_b, m0, tn * 256, acc);
                     qg_finish_at<EPI, INT8, 4>(a, lds, lds_b, m0, tn * 256, acc);
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -915,10 +918,13 @@ __device__ __forceinline__ void qg_impl_h3(const qw_gemm_args &a, unsigned char 
 }
 
 /* One LDS array fixes the layout: the first stage at offset 0, the second
- * at 64 KB, the split-tile counter after them. */
+ * at 64 KB, the split-tile counter after them; the bf16 kernels' array also
+ * holds the three 48 KB stages of the walk's half tiles (the counter, used
+ * only by split tiles, falls inside the third). */
 #define QG_ENTRY(name, EPI, INT8)                                                              \
     QW_KERNEL void __launch_bounds__(256, 1) name(qw_gemm_args a) {                            \
-        __shared__ __attribute__((aligned(16))) unsigned char smem[2 * QG_STAGE + 16];          \
+        __shared__ __attribute__((aligned(16)))                                                \
+        unsigned char smem[(INT8 ? 2 * QG_STAGE : 3 * QG3_STAGE) + 16];                        \
         qg_impl<EPI, INT8>(a, smem, smem + QG_STAGE);                                          \
     }
 

@@ -52,6 +52,8 @@ typedef struct {
      * Split tiles (split > 1, bf16 W): half_count != 0 runs them as half
      * tiles, each in `split` pieces. */
     uint32_t half_from, half_count;
+    /* the walk's half tiles on three LDS stages (bf16 W kernels) */
+    uint32_t half3;
 } qw_gemm_args;
 
 typedef struct {
