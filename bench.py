@@ -573,6 +573,9 @@ def main():
                     choices=["down", "attention"],
                     help="only launch a calibration copy and the dominant GEMM (default) or "
                          "the attention kernel, for rocprofv3 --pmc")
+    ap.add_argument("--denoise-only", action="store_true",
+                    help="only run the 8-step 512x512 denoise loop (BASELINE configs[3]) and "
+                         "print its line, for a kernel trace of that configuration")
     ap.add_argument("--vendor", action="store_true",
                     help="only time the four step linears (bf16 W) here and through "
                          "torch.matmul (hipBLASLt), alternating, and print that line")
@@ -589,6 +592,10 @@ def main():
     gpu = qd.Gpu()
     if args.vendor:
         print(json.dumps({"vendor_gemm": vendor_gemm(qd, gpu)}))
+        gpu.close()
+        return
+    if args.denoise_only:
+        print(json.dumps({"denoise_512_8step": denoise_512(qd, gpu)}))
         gpu.close()
         return
     if args.profile_kernel:
