@@ -32,6 +32,7 @@ enum {
     K_GEMM_W8_STORE_Q, K_GEMM_W8_GELU_Q, K_GEMM_W8_GATE_Q, K_GEMM_W8_QKN_Q,
     K_GEMM_BF16_STORE_T224, K_GEMM_BF16_GELU_T224, K_GEMM_BF16_GATE_T224, K_GEMM_BF16_QKN_T224,
     K_GEMM_BF16_STORE_H3, K_GEMM_BF16_GELU_H3, K_GEMM_BF16_GATE_H3, K_GEMM_BF16_QKN_H3,
+    K_ATTN_W4,
     K_COUNT
 };
 static const char *k_names[K_COUNT] = {
@@ -48,7 +49,7 @@ static const char *k_names[K_COUNT] = {
     "qw_gemm_bf16_store_t224", "qw_gemm_bf16_gelu_t224", "qw_gemm_bf16_gate_t224",
     "qw_gemm_bf16_qkn_t224",
     "qw_gemm_bf16_store_h3", "qw_gemm_bf16_gelu_h3", "qw_gemm_bf16_gate_h3",
-    "qw_gemm_bf16_qkn_h3"};
+    "qw_gemm_bf16_qkn_h3", "qw_attention_w4_bf16"};
 
 /* How int8 linears run (QW_INT8_ROUTE, a measurement switch): AUTO (the
  * default) widens the weight to a bf16 copy and runs the bf16 kernels when
@@ -72,7 +73,9 @@ struct h3_gpu {
     std::string label;
     void *scratch;
     size_t scratch_bytes;
-    uint32_t attn_threads; /* attention workgroup size, 64 per 32-query wave */
+    uint32_t attn_threads;  /* attention workgroup size, 64 per 32-query wave */
+    uint32_t attn4_threads; /* the same for the small launches' kernel */
+    int attn_small; /* launches of fewer 256-query blocks than CUs on the 4-wave kernel (QW_ATTN_W4=0: off) */
     int int8_route; /* QW_INT8_* : how int8 linears of many rows run */
     int t224;       /* 224-row tiles allowed (QW_GEMM_T224=0 turns them off, for measurement) */
     uint32_t split_min_steps, split_force; /* measurement: QW_SPLIT_MIN_STEPS, QW_SPLIT_FORCE */
@@ -219,17 +222,22 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
             return NULL;
         }
     }
-    /* The attention kernel's workgroup (its launch bound) sets the query
-     * block: one 64-lane wave per 32 queries. */
-    int attn_threads = 0;
-    e = hipFuncGetAttribute(&attn_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, g->fn[K_ATTN]);
-    if (e != hipSuccess || attn_threads < 64 || attn_threads > 1024 || attn_threads % 64) {
-        set_err(error, error_size, "qw_attention_bf16: bad workgroup bound %d", attn_threads);
-        hipModuleUnload(g->module);
-        delete g;
-        return NULL;
+    /* The attention kernels' workgroups (their launch bounds) set the query
+     * blocks: one 64-lane wave per 32 queries. */
+    for (int w = 0; w < 2; w++) {
+        const int kid = w ? K_ATTN_W4 : K_ATTN;
+        int attn_threads = 0;
+        e = hipFuncGetAttribute(&attn_threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, g->fn[kid]);
+        if (e != hipSuccess || attn_threads < 64 || attn_threads > 1024 || attn_threads % 64) {
+            set_err(error, error_size, "%s: bad workgroup bound %d", k_names[kid], attn_threads);
+            hipModuleUnload(g->module);
+            delete g;
+            return NULL;
+        }
+        (w ? g->attn4_threads : g->attn_threads) = (uint32_t)attn_threads;
     }
-    g->attn_threads = (uint32_t)attn_threads;
+    g->attn_small = 1;
+    if (const char *r = getenv("QW_ATTN_W4")) g->attn_small = atoi(r) != 0;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, g->device) != hipSuccess ||
         cus <= 0) {
@@ -1380,9 +1388,18 @@ extern "C" int qw_gpu_attention_bf16(h3_gpu *g, const qw_attention_desc *d) {
     g->stats.mps_sdpa_dispatches += 0;
     if (((uint64_t)(d->kv_rows - 1) * std::max(d->ldk, d->ldv) + hd) * 2 >= (1ull << 31))
         return fail(g, "attention: one batch entry's K/V exceed 2 GiB");
+    /* Fewer 256-query blocks than CUs: 128-query workgroups, two per CU,
+     * bring the idle CUs in (the same bits; 1 x 24 heads x 1152 rows 28.7
+     * against 44.3 us, 320 rows 13.4 against 18.8; at 2 x 24 x 4352 rows the
+     * 256-query kernel stays ahead, 391.5 against 398.9 us). */
     const uint32_t aqb = g->attn_threads / 2; /* 32 query rows per 64-lane wave */
     const uint64_t nwg = (uint64_t)((d->q_rows + aqb - 1) / aqb) * d->heads * d->batch;
     if (nwg >= (1ull << 31)) return fail(g, "attention: grid too large");
+    if (g->attn_small && nwg < g->cus) {
+        const uint32_t aqb4 = g->attn4_threads / 2;
+        const uint64_t nwg4 = (uint64_t)((d->q_rows + aqb4 - 1) / aqb4) * d->heads * d->batch;
+        return launch(g, K_ATTN_W4, dim3((uint32_t)nwg4), dim3(g->attn4_threads), a);
+    }
     return launch(g, K_ATTN, dim3((uint32_t)nwg), dim3(g->attn_threads), a);
 }
 

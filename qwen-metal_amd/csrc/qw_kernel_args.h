@@ -172,15 +172,6 @@ typedef struct {
     uint64_t count;
 } qw_zero_args;
 
-/* Waves per attention workgroup (32 queries each). The host reads the
- * workgroup size back from the code object. */
-#ifndef QW_ATTN_WAVES
-#define QW_ATTN_WAVES 8
-#endif
-/* Query rows per attention workgroup; the host derives the same number
- * from the workgroup size it reads back (32 rows per 64-lane wave) */
-#define QW_ATTN_QROWS (32 * QW_ATTN_WAVES)
-
 /* Flash attention over a joint sequence: out[b*q_rows + r] attends keys
  * [b*kv_rows, b*kv_rows + limit(r)) of the same batch entry. */
 typedef struct {

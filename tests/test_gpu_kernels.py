@@ -718,6 +718,38 @@ def test_attention_strided_qkv(gpu, qd, oracle):
                       oracle.bf16_to_f32(ref)) < 5e-3
 
 
+@pytest.mark.parametrize("rows,heads,text,causal,batch,limits", [
+    (1152, 3, 128, 0, 1, False), (320, 4, 64, 1, 1, False), (300, 2, 44, 1, 2, False),
+    (200, 2, 0, 0, 1, True), (1, 1, 0, 0, 1, False)])
+def test_attention_small_launch_kernel_bit_identical(qd, oracle, monkeypatch, rows, heads, text,
+                                                     causal, batch, limits):
+    """Launches of fewer 256-query blocks than CUs run the 128-query (4-wave)
+    kernel; every query row's arithmetic is the 256-query kernel's, so both
+    give the same bits (t2i masks, ragged rows, batch 2, a per-row limit
+    table)."""
+    H = heads * 128
+    qkv = synth(oracle, batch * rows * 3 * H, 91)
+    lim = None
+    if limits:
+        lim = np.random.default_rng(92).integers(1, rows + 1, rows).astype(np.uint32)
+    outs = []
+    for w4 in ("1", "0"):
+        monkeypatch.setenv("QW_ATTN_W4", w4)
+        g = qd.Gpu()
+        try:
+            t = g.put(qkv)
+            out = g.new(batch * rows * H, qd.BF16)
+            g.attention(out, t, t, t, batch, rows, rows, heads, 3 * H, 3 * H, 3 * H, H,
+                        q_offset=0, k_offset=H, v_offset=2 * H,
+                        kv_limit=g.put(lim) if limits else None, text_rows=text,
+                        text_causal=causal)
+            g.submit()
+            outs.append(out.read())
+        finally:
+            g.close()
+    assert np.array_equal(outs[0], outs[1])
+
+
 def test_elementwise_family(gpu, qd, oracle):
     L, OL = qd.lib(), oracle.lib()
     n = 70001
