@@ -79,6 +79,7 @@ struct h3_gpu {
     int int8_route; /* QW_INT8_* : how int8 linears of many rows run */
     int t224;       /* 224-row tiles allowed (QW_GEMM_T224=0 turns them off, for measurement) */
     uint32_t split_min_steps, split_force; /* measurement: QW_SPLIT_MIN_STEPS, QW_SPLIT_FORCE */
+    uint32_t split_small_min; /* shortest piece of a small launch (QW_SPLIT_SMALL_MIN_STEPS) */
     int half3;      /* small launches' half tiles on the three-stage kernels (QW_GEMM_HALF3=0: two) */
     int half_small; /* launches of at most cus / 2 tiles as half tiles (QW_GEMM_HALF_SMALL=0: off) */
     /* qw_gpu_span_*: event pairs recorded on the stream, read after a sync */
@@ -197,6 +198,8 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     if (const char *r = getenv("QW_GEMM_T224")) g->t224 = atoi(r) != 0;
     g->split_min_steps = 32;
     if (const char *r = getenv("QW_SPLIT_MIN_STEPS")) g->split_min_steps = (uint32_t)atoi(r);
+    g->split_small_min = 16;
+    if (const char *r = getenv("QW_SPLIT_SMALL_MIN_STEPS")) g->split_small_min = (uint32_t)atoi(r);
     g->split_force = 0;
     if (const char *r = getenv("QW_SPLIT_FORCE")) g->split_force = (uint32_t)atoi(r);
     g->half3 = 1;
@@ -973,6 +976,31 @@ static uint32_t split_choice(h3_gpu *g, uint32_t tiles, uint32_t ksteps,
     return best;
 }
 
+/* Pieces for the half tiles of a small launch (at most cus / 2 tiles), all
+ * in one round of CUs: the s that minimises 0.72 ksteps / s + 12 + 0.04
+ * units s microseconds -- a half tile's slice, then each piece's prologue,
+ * partial sums and last-piece reduction, which grow with the pieces in
+ * flight. Fitted to the three-stage kernels at K = 3072 (M = 320: 24, 48,
+ * 64, 96, 128 half tiles in 3, 3, 3, 2, 2 pieces 26.0, 29.3, 32.4, 35.8,
+ * 40.6 us against 34.7-35.6 unsplit; M = 1152: 120 in 2 pieces 38.8
+ * against 35.5), within 1.2 us of each. */
+static uint32_t small_split_choice(h3_gpu *g, uint32_t units, uint32_t ksteps) {
+    if (g->split_force > 1 && (uint64_t)units * g->split_force <= g->cus &&
+        ksteps >= g->split_force)
+        return g->split_force;
+    uint32_t best = 1;
+    double best_t = 0.72 * ksteps;
+    for (uint32_t s = 2; s <= 8; s++) {
+        if ((uint64_t)units * s > g->cus || ksteps < g->split_small_min * s) break;
+        const double t = 0.72 * ksteps / s + 12.0 + 0.04 * units * s;
+        if (t < best_t) {
+            best_t = t;
+            best = s;
+        }
+    }
+    return best;
+}
+
 /* no_alloc: the workspace-free form behind qw_gpu_linear_static (int8
  * weights always widen inside the GEMM; split-tile partials and counters live
  * in the static workspace, as far as it holds them) */
@@ -1180,11 +1208,12 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
          * partial bytes) */
         small = !(int8 && !widen) && 2 * tiles <= g->cus && g->cus % 8 == 0 && g->half_small;
         const uint32_t units = small ? 2 * tiles : tiles;
-        /* half tiles of a small launch: pieces down to 16 k-steps (M = 320,
-         * K = N = 3072: 24 half tiles in 3 pieces 33.4 us, unsplit 45.1;
-         * M = 1152: 60 in 2 pieces 45.3 against 48.1) */
-        const uint32_t s = split_choice(g, units, d->k / 64, (uint64_t)QW_SPLIT_MAX_PIECES * 1024u,
-                                        small ? 16u : 0u);
+        /* half tiles of a small launch: pieces of at least 16 k-steps, all
+         * in one round of CUs (a second round of short pieces costs more
+         * than it saves: M = 320, K = 3072, N = 10752, 168 half tiles in 3
+         * pieces 62.8 us against 37 unsplit) */
+        const uint32_t s = small ? small_split_choice(g, units, d->k / 64)
+                                 : split_choice(g, units, d->k / 64);
         if (s > 1) {
             if (!g->sk_part) {
                 hipStreamSynchronize(g->stream);
