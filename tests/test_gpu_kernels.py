@@ -483,21 +483,26 @@ def test_linear_tile_walk(gpu, qd, oracle, epi):
     assert ok.all() and np.mean(d == 0) > 0.97, (d.max(), np.mean(d == 0))
 
 
-@pytest.mark.parametrize("rows,int8,rope_rows", [(300, False, 300), (300, True, 150),
-                                                 (1000, True, 500), (4357, False, 4357),
-                                                 # tables under 128 rows: the plain
-                                                 # linear, then the standalone kernel
-                                                 (300, False, 100), (300, True, 64),
-                                                 # 270 tiles: a tile walk whose last 14
-                                                 # tiles run as half tiles
-                                                 (11400, False, 11400)])
-def test_linear_qknorm_epilogue_bit_identical(gpu, qd, oracle, rows, int8, rope_rows):
+@pytest.mark.parametrize("rows,int8,rope_rows,k", [(300, False, 300, 512), (300, True, 150, 512),
+                                                   (1000, True, 500, 512),
+                                                   (4357, False, 4357, 512),
+                                                   # tables under 128 rows: the plain
+                                                   # linear, then the standalone kernel
+                                                   (300, False, 100, 512), (300, True, 64, 512),
+                                                   # 270 tiles: a tile walk whose last 14
+                                                   # tiles run as half tiles
+                                                   (11400, False, 11400, 512),
+                                                   # a small launch's half tiles in 3
+                                                   # k-range pieces
+                                                   (300, False, 300, 3072),
+                                                   (600, True, 600, 3072)])
+def test_linear_qknorm_epilogue_bit_identical(gpu, qd, oracle, rows, int8, rope_rows, k):
     """The fused q|k|v linear with the per-head RMS norm and RoPE of q and k
     in its epilogue equals the linear followed by qw_gpu_qk_norm_rope_bf16,
     bit for bit (same sums, same reduction order, same roundings): fused
     int8 kernel, widen route, ragged rows, a RoPE table shorter than the
     rows (batched sequences), tables shorter than a wave's 128 rows."""
-    heads, k = 4, 512
+    heads = 4
     n = 3 * heads * 128
     x = synth(oracle, rows * k, 31)
     w = synth(oracle, n * k, 32, 0.02)
