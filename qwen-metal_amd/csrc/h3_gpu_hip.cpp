@@ -60,6 +60,10 @@ enum { QW_INT8_AUTO = 0, QW_INT8_WIDEN = 1, QW_INT8_W8 = 2 };
 
 #define QW_SPAN_MAX 4096
 
+/* below this many rows an int8 linear widens inside its GEMM, unless the
+ * launch is small enough for half tiles (linear_impl) */
+#define QW_WIDEN_MIN_ROWS 512
+
 struct h3_gpu {
     int device;
     hipStream_t stream;
@@ -81,6 +85,7 @@ struct h3_gpu {
     uint32_t split_min_steps, split_force; /* measurement: QW_SPLIT_MIN_STEPS, QW_SPLIT_FORCE */
     uint32_t split_small_min; /* shortest piece of a small launch (QW_SPLIT_SMALL_MIN_STEPS) */
     int half3;      /* small launches' half tiles on the three-stage kernels (QW_GEMM_HALF3=0: two) */
+    uint32_t widen_min_rows; /* int8: fewest rows for the widening route (QW_WIDEN_MIN_ROWS) */
     int half_small; /* launches of at most cus / 2 tiles as half tiles (QW_GEMM_HALF_SMALL=0: off) */
     /* qw_gpu_span_*: event pairs recorded on the stream, read after a sync */
     hipEvent_t *span_ev;
@@ -204,6 +209,8 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     if (const char *r = getenv("QW_SPLIT_FORCE")) g->split_force = (uint32_t)atoi(r);
     g->half3 = 1;
     if (const char *r = getenv("QW_GEMM_HALF3")) g->half3 = atoi(r) != 0;
+    g->widen_min_rows = QW_WIDEN_MIN_ROWS;
+    if (const char *r = getenv("QW_WIDEN_MIN_ROWS")) g->widen_min_rows = (uint32_t)atoi(r);
     g->half_small = 1;
     if (const char *r = getenv("QW_GEMM_HALF_SMALL")) g->half_small = atoi(r) != 0;
     g->cus = 0;
@@ -934,8 +941,6 @@ extern "C" int qw_gpu_widen_int8_bf16(h3_gpu *g, h3_gpu_tensor *out, const h3_gp
     return widen_launch(g, (uint16_t *)out->ptr, (const int8_t *)q->ptr, count);
 }
 
-/* below this many rows an int8 linear always widens inside its GEMM */
-#define QW_WIDEN_MIN_ROWS 512
 
 /* Split tiles. A grid of one workgroup per 256 x 256 tile runs in waves of
  * `cus` tiles; when the last wave is partly filled (R = tiles % cus tiles,
@@ -1113,7 +1118,15 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * pass plus the bf16 kernel. */
     int route = g->int8_route;
     if (route == QW_INT8_AUTO) route = d->k >= 8192 ? QW_INT8_W8 : QW_INT8_WIDEN;
-    const int widen = int8 && !no_alloc && d->rows >= QW_WIDEN_MIN_ROWS && route == QW_INT8_WIDEN;
+    /* A launch of at most cus / 2 tiles widens by a pass at any row count
+     * and K: the bf16 kernels' half tiles beat the whole "_w8" tiles by more
+     * than the pass costs (M = 64-448, us, w8 / pass + half tiles: QKV
+     * 64-66 / 48-55, out 63 / 35-38, up 65-67 / 56-59, down 74-84 / 66-76). */
+    const uint32_t tiles_w = ((d->rows + 255) / 256) * ((d->cols + 255) / 256);
+    const int small_w = g->int8_route == QW_INT8_AUTO && g->half_small && 2 * tiles_w <= g->cus;
+    if (small_w) route = QW_INT8_WIDEN;
+    const int widen = int8 && !no_alloc && (d->rows >= g->widen_min_rows || small_w) &&
+                      route == QW_INT8_WIDEN;
     const void *wptr = d->weight->ptr;
     if (widen) {
         const size_t n = (size_t)d->cols * d->k, bytes = n * 2;

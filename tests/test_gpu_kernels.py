@@ -128,6 +128,30 @@ def test_linear_store(gpu, qd, oracle, rows, k, n, bias, int8):
     assert_linear_close(oracle, got, ref.ravel(), mag)
 
 
+@pytest.mark.parametrize("rows,k,n,bias", [c[:4] for c in LINEAR_CASES if c[4] and c[0] > 8])
+def test_linear_int8_in_lds_route(qd, oracle, monkeypatch, rows, k, n, bias):
+    """The "_w8" kernels (int8 W widened in LDS inside the GEMM) on the int8
+    cases, forced by QW_INT8_ROUTE=w8: by default these small launches widen
+    by a pass and run the bf16 half tiles instead."""
+    monkeypatch.setenv("QW_INT8_ROUTE", "w8")
+    gpu = qd.Gpu()
+    try:
+        x = synth(oracle, rows * k, 1)
+        w = synth(oracle, n * k, 2, 0.02)
+        b = synth(oracle, n, 3, 0.02) if bias else None
+        q, s = oracle.quantize_int8_rows(w, n, k)
+        out = gpu.new(rows * n, qd.BF16)
+        gpu.linear(out, gpu.put(x), gpu.put(q), rows, k, n, bias=gpu.put(b) if bias else None,
+                   wscale=gpu.put(s))
+        gpu.submit()
+        ref = oracle.linear_i8(x, q, s, b, rows, k, n)
+        absx, absw = x & np.uint16(0x7FFF), w & np.uint16(0x7FFF)
+        mag = oracle.bf16_to_f32(oracle.linear(absx, absw, None, rows, k, n)).ravel()
+        assert_linear_close(oracle, out.read(), ref.ravel(), mag)
+    finally:
+        gpu.close()
+
+
 @pytest.mark.parametrize("int8,rows,rm_blocks", [(False, 300, 0), (True, 300, 0), (True, 600, 0),
                                                  (False, 4, 0), (True, 7, 0), (False, 300, 1),
                                                  (True, 600, 1)])
