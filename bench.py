@@ -15,8 +15,8 @@ hipEvents on the library's stream. Right after it, the same forwards run
 with a HIP event pair around every stage of every block on that stream
 (`in_step`, no synchronisation inside a forward); the dominant kernel's
 average there (the down-projection GEMM, M=8704 K=12288 N=3072,
-residual-gate epilogue, int8 weight widened to bf16 in LDS inside the GEMM)
-is the roofline entry's launch time. Every linear shape and the attention
+residual-gate epilogue, with the int8 weight's widening pass ahead of it
+in the same span) is the roofline entry's launch time. Every linear shape and the attention
 kernel are also timed alone, back to back, for the breakdown.
 
 cpu_baseline: the CPU oracle (oracle/, OpenMP) on BASELINE configs[0]-[2]
@@ -42,7 +42,29 @@ PEAK_HBM_GBS = 8000.0
 CFG = dict(hidden=3072, heads=24, mlp_width=12288, text_dim=4096, z_dim=64, layers=32,
            mlp_act=1, adaln_shift=1, has_bias=1, text_causal=0, int8_weights=1)
 TEXT, GH, GW, BATCH, SIGMA, SEED = 256, 64, 64, 2, 0.5, 2026
-W8_MIN_K = 8192  # int8 linears with K >= this widen in LDS inside the GEMM ("_w8")
+W8_MIN_K = 8192  # int8 linears with K >= this may widen in LDS inside the GEMM ("_w8")
+
+
+def int8_in_lds(M, K, N, cus=256):
+    """The library's automatic int8 route for an M-row linear (linear_impl
+    in h3_gpu_hip.cpp): True where the "_w8" kernels widen the weight in LDS
+    inside the GEMM, False where a widening pass runs ahead of the bf16
+    kernels (or, for at most 8 rows, the GEMV kernels widen in registers).
+    A launch of at most cus / 2 tiles widens by a pass; a larger one of
+    fewer than 512 rows stays on "_w8"; from 512 rows "_w8" needs K >= 8192
+    and a shape on which the bf16 kernels would not take 224-row tiles."""
+    tn = (N + 255) // 256
+    tiles = (M + 255) // 256 * tn
+    if M <= 8 or 2 * tiles <= cus:
+        return False
+    if M < 512:
+        return True
+    if K < W8_MIN_K:
+        return False
+    r = tiles % cus
+    w256 = tiles // cus + ((0.5 if 2 * r <= cus else 1.0) if r else 0.0)
+    w224 = 0.875 * (((M + 223) // 224 * tn + cus - 1) // cus)
+    return not w224 < 0.97 * w256
 
 
 def load_qdit():
@@ -78,12 +100,13 @@ def time_ms(gpu, fn, reps):
 
 def kernel_breakdown(qd, gpu, reps=10):
     """Each linear shape of the step and the attention kernel, alone, on the
-    library's stream. `ms` is the int8 linear as the step runs it: the down
-    projection (K = 12288) is one launch of the "_w8" kernel, which widens
-    the int8 weight in LDS; the K = 3072 linears are two launches, the
-    weight widening pass (qw_widen_i8_bf16) and the bf16 GEMM with the scale
-    in its epilogue, both also timed on their own (`widen_ms`, `gemm_ms`;
-    for the down projection `gemm_ms` is the "_w8" launch itself)."""
+    library's stream. `ms` is the int8 linear as the step runs it: at this
+    workload all four are two launches, the weight widening pass
+    (qw_widen_i8_bf16) and the bf16 GEMM with the scale in its epilogue (the
+    out and down projections on 224-row tiles), both also timed on their own
+    (`widen_ms`, `gemm_ms`); a shape the library runs on a "_w8" kernel (the
+    int8 weight widened in LDS inside the GEMM) is one launch, `gemm_ms`
+    being that launch."""
     H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
     L = qd.lib()
     a = gpu.new(M * F, qd.BF16)
@@ -109,7 +132,7 @@ def kernel_breakdown(qd, gpu, reps=10):
         gemm = lambda: gpu.linear(big, a, wb, M, k, n, wscale=s, epilogue=epi, **kw)  # noqa
         full()
         ms = time_ms(gpu, full, reps)
-        in_gemm = k >= W8_MIN_K  # the library's int8 route at these rows
+        in_gemm = int8_in_lds(M, k, n)  # the library's int8 route at these rows
         if in_gemm:
             gemm_ms, widen_ms = ms, 0.0
         else:
@@ -312,7 +335,7 @@ def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, calibrated against
     a copy kernel of known size), or None when it has not been measured."""
-    p = os.path.join(ROOT, "profiles", "gemm_down_w8_gate_q_traffic.md")
+    p = os.path.join(ROOT, "profiles", "gemm_down_int8_step_route_traffic.md")
     if not os.path.exists(p):
         return None
     with open(p) as f:
@@ -400,8 +423,9 @@ def profile_kernel(qd, gpu, reps=5):
     """Launch-only mode for rocprofv3 --pmc passes: a plain copy of a known
     size (the counter calibration: 256 MiB read + 256 MiB written), then
     the dominant GEMM -- the down projection, M=8704 K=12288 N=3072, on the
-    int8 weight (qw_gemm_w8_gate_q, widened in LDS) with the residual-gate
-    epilogue -- `reps` times. Nothing is timed or printed as a result."""
+    int8 weight with the residual-gate epilogue, as the step runs it (the
+    widening pass qw_widen_i8_bf16, then qw_gemm_bf16_gate_t224) -- `reps`
+    times. Nothing is timed or printed as a result."""
     H, F, M = CFG["hidden"], CFG["mlp_width"], BATCH * (TEXT + GH * GW)
     L = qd.lib()
     calibration_copy(qd, gpu)
@@ -645,7 +669,8 @@ def main():
     roofline = None
     if down:
         # the dominant kernel of the step (largest total time in the kernel
-        # trace): the down projection's GEMM, one launch per block, its
+        # trace): the down projection's GEMM, one launch per block (with its
+        # widening pass where the route has one: the span covers both), its
         # average over the blocks of the forwards right after the timed
         # region (HIP events on the library's stream)
         fl = 2.0 * down["M"] * down["N"] * down["K"]
@@ -653,12 +678,16 @@ def main():
         roofline = {"bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
                     "traffic": measured_traffic(),
-                    "kernel": "qw_gemm_w8_gate_q (down projection, M=8704 K=12288 N=3072, "
-                              "int8 weight widened to bf16 in LDS once per workgroup, scale "
-                              "and residual gate in the epilogue, tail tiles split in 3 "
-                              "k-ranges)",
+                    "kernel": ("qw_gemm_w8_gate_q (down projection, M=8704 K=12288 N=3072, "
+                               "int8 weight widened to bf16 in LDS once per workgroup, scale "
+                               "and residual gate in the epilogue)"
+                               if int8_in_lds(down["M"], down["K"], down["N"]) else
+                               "qw_widen_i8_bf16 + qw_gemm_bf16_gate_t224 (down projection, "
+                               "M=8704 K=12288 N=3072: the int8 weight widened to bf16 by a "
+                               "pass, then 224 x 256 tiles in 2 waves, scale and residual "
+                               "gate in the epilogue; the span covers both launches)"),
                     "flop_per_launch": fl, "ms_per_launch": down["ms"],
-                    "ms_per_launch_alone": brk["down"]["gemm_ms"] if brk else None,
+                    "ms_per_launch_alone": brk["down"]["ms"] if brk else None,
                     # A bf16 + W int8 + row scales + residual and output bf16
                     "algorithmic_bytes_per_launch": (2.0 * down["M"] * down["K"] +
                                                      down["N"] * down["K"] + 4.0 * down["N"] +

@@ -86,6 +86,7 @@ struct h3_gpu {
     uint32_t split_small_min; /* shortest piece of a small launch (QW_SPLIT_SMALL_MIN_STEPS) */
     int half3;      /* small launches' half tiles on the three-stage kernels (QW_GEMM_HALF3=0: two) */
     uint32_t widen_min_rows; /* int8: fewest rows for the widening route (QW_WIDEN_MIN_ROWS) */
+    int t224_over_split; /* 224-row tiles preferred to split tiles (QW_T224_OVER_SPLIT=0: off) */
     int half_small; /* launches of at most cus / 2 tiles as half tiles (QW_GEMM_HALF_SMALL=0: off) */
     /* qw_gpu_span_*: event pairs recorded on the stream, read after a sync */
     hipEvent_t *span_ev;
@@ -211,6 +212,8 @@ extern "C" h3_gpu *h3_gpu_create(const char *code_object_path, char *error,
     if (const char *r = getenv("QW_GEMM_HALF3")) g->half3 = atoi(r) != 0;
     g->widen_min_rows = QW_WIDEN_MIN_ROWS;
     if (const char *r = getenv("QW_WIDEN_MIN_ROWS")) g->widen_min_rows = (uint32_t)atoi(r);
+    g->t224_over_split = 1;
+    if (const char *r = getenv("QW_T224_OVER_SPLIT")) g->t224_over_split = atoi(r) != 0;
     g->half_small = 1;
     if (const char *r = getenv("QW_GEMM_HALF_SMALL")) g->half_small = atoi(r) != 0;
     g->cus = 0;
@@ -1116,13 +1119,26 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
      * VALU work (1.5 instructions per weight per workgroup): the same
      * kernel with the conversion left out runs as fast as the widening
      * pass plus the bf16 kernel. */
+    /* the 224-row tile rule on this shape (whole tiles, bf16 kernels) */
+    const uint32_t tn_w = (d->cols + 255) / 256, tiles_w = ((d->rows + 255) / 256) * tn_w;
+    const uint32_t t224_w = ((d->rows + 223) / 224) * tn_w;
+    int rule224 = 0;
+    if (g->t224 && g->cus % 8 == 0) {
+        const uint32_t C = g->cus, R = tiles_w % C;
+        const double w256 = (double)(tiles_w / C) + (R ? (2 * R <= C ? 0.5 : 1.0) : 0.0);
+        rule224 = 0.875 * (double)((t224_w + C - 1) / C) < 0.97 * w256;
+    }
+    /* K >= 8192 keeps the in-LDS widening, unless the widened weight's bf16
+     * kernel takes 224-row tiles (the down projection at M = 8704: whole
+     * steps 64.07 against 65.39 ms with the pass and 224-row tiles, medians
+     * of 8, same box, alternating) */
     int route = g->int8_route;
-    if (route == QW_INT8_AUTO) route = d->k >= 8192 ? QW_INT8_W8 : QW_INT8_WIDEN;
+    if (route == QW_INT8_AUTO)
+        route = d->k >= 8192 && !(rule224 && g->t224_over_split) ? QW_INT8_W8 : QW_INT8_WIDEN;
     /* A launch of at most cus / 2 tiles widens by a pass at any row count
      * and K: the bf16 kernels' half tiles beat the whole "_w8" tiles by more
      * than the pass costs (M = 64-448, us, w8 / pass + half tiles: QKV
      * 64-66 / 48-55, out 63 / 35-38, up 65-67 / 56-59, down 74-84 / 66-76). */
-    const uint32_t tiles_w = ((d->rows + 255) / 256) * ((d->cols + 255) / 256);
     const int small_w = g->int8_route == QW_INT8_AUTO && g->half_small && 2 * tiles_w <= g->cus;
     if (small_w) route = QW_INT8_WIDEN;
     const int widen = int8 && !no_alloc && (d->rows >= g->widen_min_rows || small_w) &&
@@ -1190,6 +1206,18 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
     a.sk_flag = NULL;
     uint32_t grid = tiles;
     int small = 0;
+    /* 224-row tiles where they leave fewer (work-weighted) waves than
+     * 256-row tiles with their half-tile tail: a wave of 224-row tiles is
+     * 0.875 of one of 256-row tiles. Out projection, M = 8704: 2 waves of
+     * 0.875 (468 tiles) against 2 waves (408 tiles). */
+    const uint32_t t224 = ((d->rows + 223) / 224) * a.tiles_n;
+    int use224 = 0;
+    if (!(int8 && !widen) && g->t224 && g->cus % 8 == 0) {
+        const uint32_t C = g->cus, R = tiles % C;
+        const double w256 = (double)(tiles / C) + (R ? (2 * R <= C ? 0.5 : 1.0) : 0.0);
+        const double w224 = 0.875 * (double)((t224 + C - 1) / C);
+        use224 = w224 < 0.97 * w256;
+    }
     if (no_alloc) {
         const uint32_t s = split_choice(g, tiles, d->k / 64, QW_STATIC_PARTS);
         if (s > 1) {
@@ -1225,8 +1253,12 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
          * in one round of CUs (a second round of short pieces costs more
          * than it saves: M = 320, K = 3072, N = 10752, 168 half tiles in 3
          * pieces 62.8 us against 37 unsplit) */
+        /* where 224-row tiles fill the waves better they also beat split
+         * tiles (down projection shape, bf16 W, M = 8704: 500 us unsplit on
+         * 224-row tiles against 568 with 256-row tiles and a 3-piece tail) */
         const uint32_t s = small ? small_split_choice(g, units, d->k / 64)
-                                 : split_choice(g, units, d->k / 64);
+                         : use224 && g->t224_over_split ? 1u
+                                                        : split_choice(g, units, d->k / 64);
         if (s > 1) {
             if (!g->sk_part) {
                 hipStreamSynchronize(g->stream);
@@ -1275,20 +1307,10 @@ static int linear_impl(h3_gpu *g, const qw_linear_desc *d, int no_alloc) {
         }
         return launch(g, kid, dim3(grid), dim3(threads), a);
     }
-    if (a.split == 1 && !(int8 && !widen) && g->t224 && g->cus % 8 == 0) {
-        /* 224-row tiles where they leave fewer (work-weighted) waves than
-         * 256-row tiles with their half-tile tail: a wave of 224-row tiles
-         * is 0.875 of one of 256-row tiles. Out projection, M = 8704: 2
-         * waves of 0.875 (468 tiles) against 2 waves (408 tiles). */
-        const uint32_t C = g->cus, R = tiles % C;
-        const uint32_t t224 = ((d->rows + 223) / 224) * a.tiles_n;
-        const double w256 = (double)(tiles / C) + (R ? (2 * R <= C ? 0.5 : 1.0) : 0.0);
-        const double w224 = 0.875 * (double)((t224 + C - 1) / C);
-        if (w224 < 0.97 * w256) {
-            a.tiles_m = (d->rows + 223) / 224;
-            return launch(g, K_GEMM_BF16_STORE_T224 + d->epilogue, dim3(t224 < C ? t224 : C),
-                          dim3(threads), a);
-        }
+    if (a.split == 1 && use224) {
+        a.tiles_m = (d->rows + 223) / 224;
+        return launch(g, K_GEMM_BF16_STORE_T224 + d->epilogue,
+                      dim3(t224 < g->cus ? t224 : g->cus), dim3(threads), a);
     }
     if (a.split == 1 && grid > g->cus && g->cus % 8 == 0) {
         grid = g->cus;
